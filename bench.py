@@ -1,0 +1,331 @@
+"""Benchmark of the LLM-inference operator path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--ops a,b]
+
+A step runs every op of the path once at its BASELINE.json config, with all
+inputs already resident in HBM (synthetic seeded data):
+  rms_norm        x fp16 [4096, 4096], eps 1e-6
+  reshape_cache   key/value fp16 [8192, 8, 128] -> 1024 blocks x 16 slots
+  causal_conv1d   x fp16 [8, 4096, 2048], width 4, bias, SiLU, final state
+  rotary          q [8192, 32, 128], k [8192, 8, 128], neox, base 1e4
+  gemv_f16_b{1,8} W fp16 [14336, 4096]
+  gemv_i8_b{1,8}  W int8 [14336, 4096] + fp16 scales
+  fa_prefill      bf16 q [4, 32, 4096, 128], k/v [4, 8, 4096, 128], causal
+  fa_decode       bf16 B=64, 1 token, paged block 16, kv_len ~ U{512..8192}
+Between two ops a 512 MiB buffer is rewritten (outside the per-op timing) so
+no op reads its inputs from the 256 MiB MALL / L2 left warm by the previous
+step.  Per-op kernel time: torch.cuda events on the stream the ops are
+enqueued on (tecoops binds the current torch stream), averaged over the K
+timed steps.
+
+Prints ONE JSON line.  `value` is flash-attention prefill TFLOP/s (causal
+FLOP count / average kernel time), the throughput figure of BASELINE.json's
+metric; `ops` lists every op's microseconds, algorithmic GB/s or TFLOP/s and
+fraction of the MI355X peak.  `roofline` is the dominant kernel's (by time).
+`cpu_baseline` times the CPU oracle (the reference algorithms restated in C)
+on the host cores on a bounded sample.
+"""
+import argparse
+import json
+import math
+import os
+import platform
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for p in (REPO, os.path.join(REPO, "teco-ops_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2516.6
+
+# FA prefill causal FLOPs: 4 * B * H * D * S(S+1)/2
+FA_B, FA_H, FA_HKV, FA_S, FA_D = 4, 32, 8, 4096, 128
+FA_PREFILL_FLOP = 4 * FA_B * FA_H * FA_D * FA_S * (FA_S + 1) // 2
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-flush", action="store_true")
+    ap.add_argument("--ops", default="")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    return ap.parse_args()
+
+
+_GEN = None
+
+
+def seeded_bits(rng, shape, kind="normal", scale=1.0, lo=0.0, hi=1.0, dtype="f16"):
+    """Seeded synthetic tensor generated on the GPU (fp32, rounded to 16 bit)."""
+    import torch
+    global _GEN
+    if _GEN is None:
+        _GEN = torch.Generator(device="cuda")
+        _GEN.manual_seed(int(rng.integers(1 << 30)))
+    if kind == "normal":
+        t = torch.randn(shape, generator=_GEN, device="cuda") * scale
+    else:
+        t = torch.rand(shape, generator=_GEN, device="cuda") * (hi - lo) + lo
+    return t.to(torch.float16 if dtype == "f16" else torch.bfloat16)
+
+
+def build_ops():
+    """Allocates every op's inputs on the GPU; returns {name: (launch, work)}."""
+    import torch
+    import tecoops
+
+    rng = np.random.default_rng(1000)
+    ops = {}
+
+    # rms_norm [4096, 4096]
+    x = seeded_bits(rng, (4096, 4096))
+    w = seeded_bits(rng, (4096,), "uniform", lo=0.5, hi=1.5)
+    y = torch.empty_like(x)
+    ops["rms_norm"] = (lambda: tecoops.rms_norm(x, w, None, y, None, 1e-6),
+                       dict(bytes=2 * 4096 * 4096 * 2 + 4096 * 2))
+
+    # reshape_and_cache
+    T, Hkv, D, NB, BS = 8192, 8, 128, 1024, 16
+    key = seeded_bits(rng, (T, Hkv, D))
+    val = seeded_bits(rng, (T, Hkv, D))
+    slots = torch.from_numpy(rng.permutation(NB * BS)[:T].astype(np.int64)).cuda()
+    kc = torch.zeros((NB, Hkv, BS, D), dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    ops["reshape_and_cache"] = (
+        lambda: tecoops.reshape_and_cache(key, val, slots, kc, vc),
+        dict(bytes=4 * T * Hkv * D * 2 + T * 8))
+
+    # causal_conv1d [8, 4096, 2048]
+    B, C, L = 8, 4096, 2048
+    cx = seeded_bits(rng, (B, C, L))
+    cw = seeded_bits(rng, (C, 4), scale=0.5)
+    cb = seeded_bits(rng, (C,))
+    co = torch.empty_like(cx)
+    cst = torch.zeros((B, 3, C), dtype=torch.float16, device="cuda")
+    ops["causal_conv1d"] = (
+        lambda: tecoops.causal_conv1d(cx, cw, cb, co, conv_states=cst),
+        dict(bytes=2 * B * C * L * 2 + C * 4 * 2 + C * 2 + B * 3 * C * 2))
+
+    # rotary
+    q = seeded_bits(rng, (8192, 32, 128))
+    k = seeded_bits(rng, (8192, 8, 128))
+    pos = torch.from_numpy((np.arange(8192) % 2048).astype(np.int64)).cuda()
+    ops["rotary"] = (lambda: tecoops.rotary_embedding(pos, q, k, 128),
+                     dict(bytes=2 * (q.numel() + k.numel()) * 2 + 8192 * 8))
+
+    # GEMV
+    N, K = 14336, 4096
+    W = seeded_bits(rng, (N, K), scale=0.02)
+    Wq = torch.from_numpy(rng.integers(-127, 128, (N, K), dtype=np.int8)).cuda()
+    sc = seeded_bits(rng, (N,), "uniform", lo=0.001, hi=0.01)
+    for b in (1, 8):
+        xv = seeded_bits(rng, (b, K))
+        yv = torch.empty((b, N), dtype=torch.float16, device="cuda")
+        ops[f"gemv_f16_b{b}"] = ((lambda xv=xv, yv=yv: tecoops.gemv(W, xv, yv)),
+                                 dict(bytes=N * K * 2 + b * K * 2 + b * N * 2))
+        ops[f"gemv_i8_b{b}"] = ((lambda xv=xv, yv=yv: tecoops.gemv_int8(Wq, sc, xv, yv)),
+                                dict(bytes=N * K + N * 2 + b * K * 2 + b * N * 2))
+
+    # flash attention prefill: identity block tables over 4 x 256 blocks
+    nbp = FA_S // 16
+    fq = seeded_bits(rng, (FA_B * FA_S, FA_H, FA_D), dtype="bf16")
+    fk = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
+    fv = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
+    fo = torch.empty_like(fq)
+    bt = torch.arange(FA_B * nbp, dtype=torch.int32, device="cuda").view(FA_B, nbp)
+    cu = torch.arange(0, FA_B + 1, dtype=torch.int32, device="cuda") * FA_S
+    sk = torch.full((FA_B,), FA_S, dtype=torch.int32, device="cuda")
+    scale = 1.0 / math.sqrt(FA_D)
+    ops["fa_prefill"] = (
+        lambda: tecoops.flash_attn_varlen_func(fq, fk, fv, FA_S, cu, FA_S, None, sk, scale, True,
+                                               None, bt, False, fo),
+        dict(flops=FA_PREFILL_FLOP, bytes=(fq.numel() * 2 + fk.numel() * 2) * 2))
+
+    # flash attention decode: B=64, seeded lengths U{512..8192}, shuffled blocks
+    DB = 64
+    lens = rng.integers(512, 8193, DB)
+    nblk = (lens + 15) // 16
+    tot = int(nblk.sum())
+    perm = rng.permutation(tot)
+    btd = np.zeros((DB, 512), np.int32)
+    i = 0
+    for b in range(DB):
+        btd[b, :nblk[b]] = perm[i:i + nblk[b]]
+        i += nblk[b]
+    dq = seeded_bits(rng, (DB, FA_H, FA_D), dtype="bf16")
+    dk = seeded_bits(rng, (tot, FA_HKV, 16, FA_D), dtype="bf16")
+    dv = seeded_bits(rng, (tot, FA_HKV, 16, FA_D), dtype="bf16")
+    do = torch.empty_like(dq)
+    dbt = torch.from_numpy(btd).cuda()
+    dcu = torch.arange(0, DB + 1, dtype=torch.int32, device="cuda")
+    dsk = torch.from_numpy(lens.astype(np.int32)).cuda()
+    sum_l = int(lens.sum())
+    ops["fa_decode"] = (
+        lambda: tecoops.flash_attn_varlen_func(dq, dk, dv, 1, dcu, int(lens.max()), None, dsk,
+                                               scale, True, None, dbt, False, do),
+        dict(bytes=4096 * sum_l + 2 * dq.numel() * 2 + DB * 512 * 4,
+             flops=4 * FA_H * FA_D * sum_l, sum_kv=sum_l))
+    return ops
+
+
+def cpu_baseline(threads):
+    """Times the CPU oracle (C restatement of the reference's CPU paths) on one
+    (batch, kv-group) slice of the FA prefill config: 4 query heads x 4096
+    rows, causal; reported as TFLOP/s of that slice."""
+    from oracle import oracle as orc
+    if threads > 0:
+        orc.set_threads(threads)
+    used = orc.get_threads()
+    rng = np.random.default_rng(7)
+    S, D, Hkv, H = FA_S, FA_D, FA_HKV, FA_H
+    nbp = S // 16
+    q = orc.from_float(rng.standard_normal((S, H, D), dtype=np.float32), orc.BF16)
+    kc = orc.from_float(rng.standard_normal((nbp, Hkv, 16, D), dtype=np.float32), orc.BF16)
+    vc = orc.from_float(rng.standard_normal((nbp, Hkv, 16, D), dtype=np.float32), orc.BF16)
+    bt = np.arange(nbp, dtype=np.int32)[None]
+    G = H // Hkv
+    flop = 4 * G * D * S * (S + 1) // 2
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        orc.flash_attention(q, kc, vc, bt, [S], [S], dtype=orc.BF16, b_only=0, h_begin=0, h_end=G)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    return {"value": flop / t / 1e12, "unit": "TFLOP/s", "cores": used, "kind": "port",
+            "sample": f"oracle flash_attention, 1 (batch, kv-group) slice of the prefill config "
+                      f"({G} heads x {S} rows, causal, bf16 in / fp32 math), median of 3 "
+                      f"= {t:.3f} s; the full config is 32x this work",
+            "cpu_model": cpu_model()}
+
+
+def cpu_model():
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return platform.processor()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only (no multi-GPU path); "
+                                   "run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+    torch.cuda.set_device(0)
+    ops = build_ops()
+    if args.ops:
+        keep = set(args.ops.split(","))
+        ops = {k: v for k, v in ops.items() if k in keep}
+    flush = None if args.no_flush else torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+
+    def run_step(events=None):
+        for name, (fn, _) in ops.items():
+            if flush is not None:
+                flush.zero_()
+            if events is not None:
+                events[name][0].record()
+            fn()
+            if events is not None:
+                events[name][1].record()
+
+    for _ in range(args.warmup):
+        run_step()
+    torch.cuda.synchronize()
+    ev = {n: [] for n in ops}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        e = {n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for n in ops}
+        run_step(e)
+        for n in ops:
+            ev[n].append(e[n])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    report = {}
+    for n, (_, work) in ops.items():
+        ms = [a.elapsed_time(b) for a, b in ev[n]]
+        us = 1e3 * float(np.mean(ms))
+        r = {"us": round(us, 3), "us_median": round(1e3 * float(np.median(ms)), 3)}
+        if "flops" in work and n == "fa_prefill":
+            tf = work["flops"] / (us * 1e-6) / 1e12
+            r.update(tflops=round(tf, 2), frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4), bound="mfma")
+        else:
+            gbs = work["bytes"] / (us * 1e-6) / 1e9
+            r.update(gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4), bound="hbm")
+        r["algorithmic_bytes"] = work["bytes"]
+        if "flops" in work:
+            r["algorithmic_flops"] = work["flops"]
+        if "sum_kv" in work:
+            r["sum_kv_len"] = work["sum_kv"]
+        report[n] = r
+
+    dom = max(report, key=lambda n: report[n]["us"])
+    d = report[dom]
+    if d["bound"] == "mfma":
+        roof = {"bound": "mfma", "achieved": d["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": d["frac"]}
+    else:
+        roof = {"bound": "hbm", "achieved": d["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": d["frac"]}
+    roof["kernel"] = dom
+    roof["traffic"] = traffic_for(dom)
+
+    value = report["fa_prefill"]["tflops"] if "fa_prefill" in report else None
+    line = {
+        "metric": "per-op µs + HBM GB/s vs peak; flash-attn prefill TFLOP/s vs MFMA peak",
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * wall / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 (flash attention); fp16 / int8-weight (other ops)",
+        "data": "synthetic seeded inputs of the BASELINE.json shapes, resident in HBM",
+        "config": {
+            "workload": "teco-ops LLM-inference operator path, one pass of every BASELINE.json "
+                        "config per step (value: flash-attention prefill bf16 B4 H32 Hkv8 "
+                        "S4096 D128 causal)",
+            "fa_prefill": "q [4,32,4096,128], kv [4,8,4096,128], causal, scale 1/sqrt(128)",
+            "fa_decode": "B=64, H=32, Hkv=8, D=128, block 16, kv_len seeded U{512..8192}",
+            "l2_flush_between_ops": flush is not None,
+        },
+        "ops": report,
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_threads)
+    print(json.dumps(line), flush=True)
+
+
+def traffic_for(kernel):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the
+    copy-kernel calibration), or None when not measured."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel, {}).get("hbm_bytes")
+    except (OSError, ValueError):
+        return None
+
+
+if __name__ == "__main__":
+    main()

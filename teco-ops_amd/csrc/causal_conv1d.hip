@@ -1,0 +1,241 @@
+// causal_conv1d.hip — depthwise causal 1-D convolution (+bias, SiLU) with
+// conv-state carry.
+//
+// Semantics (teco/ual/kernel/causal_conv1d/causal_conv1d.scpp:56-116 and the
+// CPU baseline test/zoo/teco/causal_conv1d/causal_conv1d.py:44-122):
+//   per sequence b with cache index c = cache_indices[b] (identity if NULL),
+//   skipped when c == pad_slot_id or its length is 0;
+//   full_x = [prefix (W-1 values), x_b],  prefix = conv_state[c] when
+//   api_mode == 1 or has_initial_state[b] != 0, else zeros;
+//   out[t, d] = act(sum_k full_x[t + k, d] * w[k, d] + bias[d])   (fp32 acc)
+//   conv_state[c] = last W-1 entries of full_x.
+// act is SiLU (v / (1 + exp(-v))); the reference always applies it.
+//
+// gfx950 design: every lane owns one channel d of one sequence and a chunk of
+// CH consecutive tokens; it loads its chunk plus the W-1 preceding inputs into
+// registers (a sliding window), so each input is fetched from HBM once and the
+// W-1 overlap comes from L1/L2.  Two lane mappings:
+//   SEQ_CONTIG (token stride 1, e.g. [batch, dim, seqlen]): consecutive lanes
+//     take consecutive chunks of one channel -> 16-byte loads/stores;
+//   otherwise (e.g. [tokens, dim]): consecutive lanes take consecutive
+//     channels of one chunk -> coalesced 2-byte accesses.
+// Only the chunk-0 lane of a (sequence, channel) touches conv_state, reading
+// the old state before writing the new one, so there is no cross-lane race.
+// HBM-bound: algorithmic bytes = 2 * (x + out) + weights + bias + state.
+#include "common.h"
+#include "device.h"
+
+namespace {
+
+using namespace tecoops::dev;
+
+struct ConvArgs {
+    int batch, seq_len, dim;
+    const uint16_t *x;
+    long long xb, xs, xd;
+    uint16_t *out;
+    long long ob, os, od;
+    const uint16_t *w;
+    int wd, ww;
+    const uint16_t *bias;
+    uint16_t *state;
+    int state_stride;
+    const int *qsl;
+    const int *cidx;
+    const int8_t *hinit;
+    int pad_slot_id, api_mode, silu;
+    int nchunks;
+};
+
+__device__ __forceinline__ float act(float v, int silu) {
+    return silu ? v / (1.0f + expf(-v)) : v;
+}
+
+template <int W, bool SEQ_CONTIG, int CH>
+__global__ void __launch_bounds__(256) conv1d_kernel(ConvArgs a) {
+    const long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    int b, d, c;
+    if (SEQ_CONTIG) {  // chunk fastest
+        c = static_cast<int>(idx % a.nchunks);
+        const long long r = idx / a.nchunks;
+        d = static_cast<int>(r % a.dim);
+        b = static_cast<int>(r / a.dim);
+    } else {  // channel fastest
+        d = static_cast<int>(idx % a.dim);
+        const long long r = idx / a.dim;
+        c = static_cast<int>(r % a.nchunks);
+        b = static_cast<int>(r / a.nchunks);
+    }
+    if (b >= a.batch) return;
+    long long len, xoff, ooff;
+    if (a.qsl != nullptr) {
+        const long long s = a.qsl[b];
+        len = a.qsl[b + 1] - s;
+        xoff = s * a.xs;
+        ooff = s * a.os;
+    } else {
+        len = a.seq_len;
+        xoff = b * a.xb;
+        ooff = b * a.ob;
+    }
+    const int cidx = a.cidx ? a.cidx[b] : b;
+    if (cidx == a.pad_slot_id) return;
+    const long long t0 = static_cast<long long>(c) * CH;
+    if (t0 >= len) return;
+    const uint16_t *xr = a.x + xoff + d * a.xd;
+    uint16_t *outr = a.out + ooff + d * a.od;
+    const bool use_state =
+        a.state != nullptr && (a.api_mode == 1 || (a.hinit != nullptr && a.hinit[b] != 0));
+    uint16_t *st = a.state ? a.state + static_cast<long long>(cidx) * a.state_stride + d : nullptr;
+
+    float wv[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
+    const float bv = a.bias ? h2f(a.bias[d]) : 0.0f;
+
+    // win[k] = full_x value at sequence position t0 - (W-1) + k
+    float win[W - 1 + CH];
+    uint16_t prefix[W - 1];  // old state values, used when t0 == 0
+#pragma unroll
+    for (int k = 0; k < W - 1; ++k)
+        prefix[k] = (t0 == 0 && use_state) ? st[static_cast<long long>(k) * a.dim] : 0;
+#pragma unroll
+    for (int k = 0; k < W - 1; ++k) {
+        const long long tt = t0 - (W - 1) + k;
+        win[k] = tt >= 0 ? h2f(xr[tt * a.xs]) : h2f(prefix[k]);
+    }
+    const bool full = t0 + CH <= len;
+    if (SEQ_CONTIG && full && tecoops::aligned(xr + t0, 16)) {
+#pragma unroll
+        for (int v = 0; v < CH / 8; ++v) {
+            const uint4 q = *reinterpret_cast<const uint4 *>(xr + t0 + 8 * v);
+            const uint32_t *pq = reinterpret_cast<const uint32_t *>(&q);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                win[W - 1 + 8 * v + 2 * j] = lo<f16>(pq[j]);
+                win[W - 1 + 8 * v + 2 * j + 1] = hi<f16>(pq[j]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+            win[W - 1 + j] = (t0 + j < len) ? h2f(xr[(t0 + j) * a.xs]) : 0.0f;
+    }
+
+    float o[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < W; ++k) acc += win[j + k] * wv[k];
+        o[j] = act(acc + bv, a.silu);
+    }
+    if (SEQ_CONTIG && full && tecoops::aligned(outr + t0, 16)) {
+#pragma unroll
+        for (int v = 0; v < CH / 8; ++v) {
+            uint4 q;
+            uint32_t *pq = reinterpret_cast<uint32_t *>(&q);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pq[j] = pack<f16>(o[8 * v + 2 * j], o[8 * v + 2 * j + 1]);
+            *reinterpret_cast<uint4 *>(outr + t0 + 8 * v) = q;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+            if (t0 + j < len) outr[(t0 + j) * a.os] = f2h(o[j]);
+    }
+
+    if (c == 0 && st != nullptr) {
+        uint16_t ns[W - 1];
+#pragma unroll
+        for (int k = 0; k < W - 1; ++k) {
+            const long long src = len - (W - 1) + k;
+            ns[k] = src >= 0 ? xr[src * a.xs] : prefix[W - 1 + src];
+        }
+#pragma unroll
+        for (int k = 0; k < W - 1; ++k) st[static_cast<long long>(k) * a.dim] = ns[k];
+    }
+}
+
+template <int W>
+void launch(const ConvArgs &a0, bool seq_contig, long long max_len, hipStream_t s) {
+    ConvArgs a = a0;
+    if (seq_contig) {
+        constexpr int CH = 8;
+        a.nchunks = static_cast<int>((max_len + CH - 1) / CH);
+        const long long total = static_cast<long long>(a.batch) * a.dim * a.nchunks;
+        hipLaunchKernelGGL((conv1d_kernel<W, true, CH>), dim3(tecoops::ceil_div(total, 256)),
+                           dim3(256), 0, s, a);
+    } else {
+        constexpr int CH = 16;
+        a.nchunks = static_cast<int>((max_len + CH - 1) / CH);
+        const long long total = static_cast<long long>(a.batch) * a.dim * a.nchunks;
+        hipLaunchKernelGGL((conv1d_kernel<W, false, CH>), dim3(tecoops::ceil_div(total, 256)),
+                           dim3(256), 0, s, a);
+    }
+}
+
+}  // namespace
+
+extern "C" tecoopsStatus_t tecoopsCausalConv1dEx(
+    tecoopsHandle_t handle, int batch, int seqLen, int dim, int width, const void *x,
+    long long xBatchStride, long long xSeqStride, long long xDimStride, void *out,
+    long long outBatchStride, long long outSeqStride, long long outDimStride, const void *weight,
+    int wDimStride, int wWidthStride, const void *bias, void *convState, int convStateStride,
+    const int *queryStartLoc, const int *convStateIndices, const int8_t *hasInitialState,
+    int padSlotId, int api_mode, int silu) {
+    // Argument checks of reference causal_conv1d.cpp:39-54, plus the width
+    // range this library supports and a usable sequence-length bound.
+    if (handle == nullptr) return TECOOPS_STATUS_NOT_INITIALIZED;
+    if (x == nullptr || weight == nullptr || out == nullptr) return TECOOPS_STATUS_BAD_PARAM;
+    if (batch <= 0 || seqLen <= 0 || dim <= 0 || width <= 0) return TECOOPS_STATUS_BAD_PARAM;
+    if (width < 2 || width > 4) {
+        TECO_ERROR("causal_conv1d: width %d not supported (2..4)", width);
+        return TECOOPS_STATUS_NOT_SUPPORTED;
+    }
+    ConvArgs a{};
+    a.batch = batch;
+    a.seq_len = seqLen;
+    a.dim = dim;
+    a.x = static_cast<const uint16_t *>(x);
+    a.xb = xBatchStride; a.xs = xSeqStride; a.xd = xDimStride;
+    a.out = static_cast<uint16_t *>(out);
+    a.ob = outBatchStride; a.os = outSeqStride; a.od = outDimStride;
+    a.w = static_cast<const uint16_t *>(weight);
+    a.wd = wDimStride; a.ww = wWidthStride;
+    a.bias = static_cast<const uint16_t *>(bias);
+    a.state = static_cast<uint16_t *>(convState);
+    a.state_stride = convStateStride;
+    a.qsl = queryStartLoc;
+    a.cidx = convStateIndices;
+    a.hinit = hasInitialState;
+    a.pad_slot_id = padSlotId;
+    a.api_mode = api_mode;
+    a.silu = silu != 0;
+    const bool seq_contig = xSeqStride == 1 && outSeqStride == 1;
+    switch (width) {
+        case 2: launch<2>(a, seq_contig, seqLen, handle->stream); break;
+        case 3: launch<3>(a, seq_contig, seqLen, handle->stream); break;
+        default: launch<4>(a, seq_contig, seqLen, handle->stream); break;
+    }
+    TECO_CHECK_LAUNCH("causal_conv1d");
+    return TECOOPS_STATUS_SUCCESS;
+}
+
+extern "C" tecoopsStatus_t tecoopsCausalConv1d(
+    tecoopsHandle_t handle, int batch, int totalSeqLen, int dim, int width, int convStateStride,
+    int xSeqStride, int outSeqStride, int padSlotId, int api_mode, int actMode, const void *x,
+    void *convState, const void *weight, void *out, const int *queryStartLoc,
+    const int *convStateIndices, const int8_t *hasInitialState) {
+    (void)actMode;  // ignored: SiLU always applied (reference causal_conv1d.scpp:110)
+    if (handle == nullptr) return TECOOPS_STATUS_NOT_INITIALIZED;
+    if (x == nullptr || weight == nullptr || out == nullptr) return TECOOPS_STATUS_BAD_PARAM;
+    if (batch <= 0 || totalSeqLen <= 0 || dim <= 0 || width <= 0) return TECOOPS_STATUS_BAD_PARAM;
+    // Layout [totalSeqLen, dim]; without queryStartLoc sequence b is the single
+    // token at row b (reference causal_conv1d.scpp:58-60).
+    const int seq_len_bound = queryStartLoc ? totalSeqLen : 1;
+    return tecoopsCausalConv1dEx(handle, batch, seq_len_bound, dim, width, x, xSeqStride,
+                                 xSeqStride, 1, out, outSeqStride, outSeqStride, 1, weight, 1,
+                                 dim, nullptr, convState, convStateStride, queryStartLoc,
+                                 convStateIndices, hasInitialState, padSlotId, api_mode, 1);
+}

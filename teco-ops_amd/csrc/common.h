@@ -1,0 +1,85 @@
+// common.h — host-side internals shared by the tecoops library sources.
+//
+// The handle replaces the reference's tecoopsContext{spa_num, spe_num,
+// spm_size, stream} (teco/interface/include/builtin_type.h:33-38): on gfx950
+// there is no SPA/SPE/SPM to describe, so the handle holds the HIP stream and
+// a grow-only device scratch buffer (allocated on the device current at the
+// first op that needs it) used by split-KV flash attention when the caller
+// passes no workspace.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdint>
+#include <cstring>
+
+#include "tecoops.h"
+
+struct tecoopsContext {
+    hipStream_t stream = nullptr;
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+
+// Descriptor: same fields and stride rules as the reference
+// (teco/interface/common/tensor.h; tecoops.cpp:70-237).  Dims beyond
+// TECOOPS_DIM_MAX live in heap arrays owned (and freed) by the descriptor.
+struct tecoopsTensorStruct {
+    tecoopsDataType_t dataType = TECOOPS_DATA_FLOAT;
+    tecoopsTensorFormat_t format = TECOOPS_TENSOR_NCHW;
+    int nbDims = 0;
+    int dims_inline[TECOOPS_DIM_MAX] = {0};
+    int strides_inline[TECOOPS_DIM_MAX] = {0};
+    int *dimA = dims_inline;
+    int *strideA = strides_inline;
+    int *expand_dims = nullptr;
+    int *expand_strides = nullptr;
+};
+
+namespace tecoops {
+
+#define TECO_ERROR(...)                                        \
+    do {                                                       \
+        std::fprintf(stderr, "[tecoops] error: " __VA_ARGS__); \
+        std::fputc('\n', stderr);                              \
+    } while (0)
+
+// Checks the launch that was just enqueued; the reference returns SUCCESS
+// unconditionally after its launch (teco/ual/ops/base_op.hpp:72-73), this
+// library maps a launch failure to TECOOPS_STATUS_INTERNAL_ERROR.
+#define TECO_CHECK_LAUNCH(what)                                                   \
+    do {                                                                          \
+        hipError_t _e = hipGetLastError();                                        \
+        if (_e != hipSuccess) {                                                   \
+            TECO_ERROR("%s launch failed: %s", what, hipGetErrorString(_e));      \
+            return TECOOPS_STATUS_INTERNAL_ERROR;                                 \
+        }                                                                         \
+    } while (0)
+
+#define TECO_RETURN_IF(cond, status, ...) \
+    do {                                  \
+        if (cond) {                       \
+            TECO_ERROR(__VA_ARGS__);      \
+            return status;                \
+        }                                 \
+    } while (0)
+
+inline bool is_16bit_float(tecoopsDataType_t t) {
+    return t == TECOOPS_DATA_HALF || t == TECOOPS_DATA_BFLOAT16;
+}
+
+__host__ __device__ inline bool aligned(const void *p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+inline unsigned ceil_div(long long a, long long b) {
+    return static_cast<unsigned>((a + b - 1) / b);
+}
+
+// Returns a device buffer of at least `bytes` owned by the handle.  Growing
+// synchronises the handle's stream first so a buffer still read by enqueued
+// work is never freed.
+tecoopsStatus_t handle_scratch(tecoopsHandle_t handle, size_t bytes, void **out);
+
+}  // namespace tecoops

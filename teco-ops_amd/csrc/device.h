@@ -1,0 +1,80 @@
+// device.h — gfx950 device helpers shared by the kernels: 16-bit float
+// element types, conversions, 128-bit vector access and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace tecoops {
+namespace dev {
+
+// Element tags: the kernels move 16-bit floats as raw bits and convert to fp32
+// for arithmetic.
+struct f16 {};
+struct bf16 {};
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return static_cast<float>(v);
+}
+
+__device__ __forceinline__ uint16_t f2h(float f) {
+    _Float16 v = static_cast<_Float16>(f);  // v_cvt_f16_f32, round to nearest even
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+__device__ __forceinline__ float b2f(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f2b(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T> struct Cvt;
+template <> struct Cvt<f16> {
+    static __device__ __forceinline__ float to(uint16_t v) { return h2f(v); }
+    static __device__ __forceinline__ uint16_t from(float f) { return f2h(f); }
+};
+template <> struct Cvt<bf16> {
+    static __device__ __forceinline__ float to(uint16_t v) { return b2f(v); }
+    static __device__ __forceinline__ uint16_t from(float f) { return f2b(f); }
+};
+
+// Low / high 16-bit halves of a packed dword as fp32.
+template <typename T>
+__device__ __forceinline__ float lo(uint32_t w) { return Cvt<T>::to(static_cast<uint16_t>(w)); }
+template <typename T>
+__device__ __forceinline__ float hi(uint32_t w) { return Cvt<T>::to(static_cast<uint16_t>(w >> 16)); }
+
+template <typename T>
+__device__ __forceinline__ uint32_t pack(float a, float b) {
+    return static_cast<uint32_t>(Cvt<T>::from(a)) | (static_cast<uint32_t>(Cvt<T>::from(b)) << 16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+}  // namespace dev
+}  // namespace tecoops

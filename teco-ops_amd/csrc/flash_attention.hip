@@ -1,0 +1,725 @@
+// flash_attention.hip — paged, varlen, causal, GQA attention on gfx950 MFMA.
+//
+// Semantics (teco/interface/ops/flash_attention.cpp:71-119,
+// teco/ual/kernel/flash_attention/flash_attention.scpp:179-416, CPU baseline
+// test/zoo/teco/flash_attention/flash_attention.py:79-140):
+//   for sequence b with q_len L and kv_len S, query row i (0-based in its
+//   chunk) sits at causal position q_start + i, q_start = max(S - L, 0)
+//   (bottom-right alignment) and sees keys j <= q_start + i, j < S.  Head h
+//   reads kv head h / (H / Hkv).  O = softmax(scale * Q K^T + mask) V with an
+//   fp32 online softmax whose running max is clamped at >= 0 (scpp:149), P
+//   rounded to the element type before the PV product (scpp:316-329), and
+//   rows with no visible key written as 0 (scpp:388).
+//   K/V are read from the paged caches [num_blocks, Hkv, block_size, D]
+//   through block_table[b][j / block_size].
+//
+// gfx950 design (one wave = 64 lanes; v_mfma_f32_32x32x16_{bf16,f16}):
+//   * Scores are computed transposed, S^T = K Q^T, so each lane owns one query
+//     column (lane % 32) and 16 key rows per 32x32 block: the row max / sum of
+//     the online softmax is a lane-local reduction plus one exchange with the
+//     other half-wave.  P^T stays in registers and is directly the B operand
+//     of O^T += V^T P^T (the key order inside an MFMA k-step is permuted
+//     consistently on both operands).
+//   * K tiles are staged in LDS row-major with a 16-byte row pad (conflict-free
+//     128-bit A-operand reads); V tiles are staged transposed (V^T[d][key],
+//     4-element pad) so the A operand of the PV product is two 64-bit reads.
+//     Global -> register prefetch of the next tile overlaps the current tile's
+//     MFMA work.
+//   * Prefill: a workgroup of 4 waves shares each K/V tile among up to 4 query
+//     heads of one GQA group (HW heads x (4/HW) row blocks of 32).  The grid
+//     walks query tiles heaviest-first and keeps all tiles of one (batch, kv
+//     head) on the same XCD (workgroup index % 8 depends only on (b, kv head)
+//     when B*Hkv*groups is a multiple of 8), so K/V are re-read from that
+//     XCD's L2.  MFMA-bound: 4*D*visible(q, k) FLOP per (q row, head).
+//   * Decode (G * q_len <= 32): the 32 MFMA columns hold every (head, row) of
+//     a GQA group; 4 waves split each 128-key tile and the key range is split
+//     across workgroups (split-KV), partial (m, l, O) merged first in LDS and
+//     then by a combine kernel.  HBM-bound: every cached K/V byte is read
+//     once.
+#include <cmath>
+
+#include "common.h"
+#include "device.h"
+
+namespace {
+
+using namespace tecoops::dev;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+template <typename T> struct Mma;
+template <> struct Mma<bf16> {
+    static __device__ __forceinline__ f32x16_t run(const uint4 &a, const uint4 &b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+        float2_t v = {a, b};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf162_t));
+    }
+};
+template <> struct Mma<f16> {
+    static __device__ __forceinline__ f32x16_t run(const uint4 &a, const uint4 &b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+        float2_t v = {a, b};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
+    }
+};
+
+constexpr float kNegInf = -INFINITY;
+
+struct FaParams {
+    const uint16_t *q;
+    const uint16_t *kc;
+    const uint16_t *vc;
+    uint16_t *o;
+    const int *bt;
+    long long bt_stride;
+    const int *q_lens;   // per-sequence q lengths, or NULL
+    const int *cu_q;     // cumulative q offsets [batch+1], used when q_lens is NULL
+    const int *kv_lens;
+    int batch, H, Hkv, G, bs, num_blocks;
+    float scale_log2;    // softmax_scale * log2(e)
+    int causal;
+    // split-KV decode
+    float *ws_o;         // [B][Hkv][max_splits][ncols][D]
+    float *ws_ml;        // [B][Hkv][max_splits][ncols][2]
+    int split_len, max_splits, rq, ncols;
+};
+
+__device__ __forceinline__ void seq_info(const FaParams &p, int b, long long &q_off, int &L) {
+    if (p.q_lens == nullptr) {
+        q_off = p.cu_q[b];
+        L = p.cu_q[b + 1] - p.cu_q[b];
+    } else {
+        long long off = 0;
+        for (int i = 0; i < b; ++i) off += p.q_lens[i];
+        q_off = off;
+        L = p.q_lens[b];
+    }
+}
+
+// Address of key row `kv` of kv head `kvh` of sequence b in a paged cache, or
+// nullptr when the row is beyond `kv_limit` or its page id is out of range.
+template <int D>
+__device__ __forceinline__ const uint16_t *kv_row(const FaParams &p, const uint16_t *cache,
+                                                  const int *bt_row, int kvh, int kv,
+                                                  int kv_limit) {
+    if (kv >= kv_limit) return nullptr;
+    const int page = bt_row[kv / p.bs];
+    if (page < 0 || page >= p.num_blocks) return nullptr;
+    return cache + ((static_cast<long long>(page) * p.Hkv + kvh) * p.bs + kv % p.bs) * D;
+}
+
+// Cooperative global -> register -> LDS staging of one TILE-key K/V tile by NT
+// threads.  K is stored row-major [TILE][D + 8]; V transposed [D][TILE + 4].
+template <int D, int TILE, int NT>
+struct TileLoader {
+    static constexpr int KP = D + 8;
+    static constexpr int VP = TILE + 4;
+    static constexpr int KCH = TILE * (D / 8) / NT;                 // K chunks per thread
+    static constexpr int VTASKS = (TILE / 4) * (D / 8);            // 4 rows x 8 cols each
+    static constexpr int VPT = (VTASKS + NT - 1) / NT;
+    static_assert(TILE * (D / 8) % NT == 0, "K tile must split evenly");
+    uint4 k[KCH];
+    uint4 v[VPT][4];
+
+    __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, int kvh, int j0,
+                                         int kv_limit) {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + i * NT;
+            const int row = c / (D / 8), col = c % (D / 8);
+            const uint16_t *src = kv_row<D>(p, p.kc, bt_row, kvh, j0 + row, kv_limit);
+            k[i] = src ? *reinterpret_cast<const uint4 *>(src + col * 8) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int task = tid + i * NT;
+            const int rg = task % (TILE / 4), cg = task / (TILE / 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint16_t *src = task < VTASKS
+                    ? kv_row<D>(p, p.vc, bt_row, kvh, j0 + 4 * rg + r, kv_limit) : nullptr;
+                v[i][r] = src ? *reinterpret_cast<const uint4 *>(src + cg * 8)
+                              : make_uint4(0, 0, 0, 0);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(uint16_t *Ks, uint16_t *Vt) const {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + i * NT;
+            const int row = c / (D / 8), col = c % (D / 8);
+            *reinterpret_cast<uint4 *>(Ks + row * KP + col * 8) = k[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int task = tid + i * NT;
+            if (task >= VTASKS) continue;
+            const int rg = task % (TILE / 4), cg = task / (TILE / 4);
+            const uint32_t *r0 = reinterpret_cast<const uint32_t *>(&v[i][0]);
+            const uint32_t *r1 = reinterpret_cast<const uint32_t *>(&v[i][1]);
+            const uint32_t *r2 = reinterpret_cast<const uint32_t *>(&v[i][2]);
+            const uint32_t *r3 = reinterpret_cast<const uint32_t *>(&v[i][3]);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                // columns d = 8cg + 2w (low halves) and 8cg + 2w + 1 (high halves)
+                uint2 lo2, hi2;
+                lo2.x = (r0[w] & 0xffffu) | (r1[w] << 16);
+                lo2.y = (r2[w] & 0xffffu) | (r3[w] << 16);
+                hi2.x = (r0[w] >> 16) | (r1[w] & 0xffff0000u);
+                hi2.y = (r2[w] >> 16) | (r3[w] & 0xffff0000u);
+                *reinterpret_cast<uint2 *>(Vt + (8 * cg + 2 * w) * VP + 4 * rg) = lo2;
+                *reinterpret_cast<uint2 *>(Vt + (8 * cg + 2 * w + 1) * VP + 4 * rg) = hi2;
+            }
+        }
+    }
+};
+
+// One wave's online-softmax attention over NKB 32-key blocks staged in LDS at
+// rows [kv_row0, kv_row0 + 32*NKB), absolute key index j_abs0 for kv_row0.
+// Lane l owns query column (l % 32) of each of its QSUB column blocks.
+//   qf:   Q^T B-operand fragments (8 x 16-bit per lane per 16-dim k-step)
+//   oacc: O^T accumulators, element v of block db is d = 32db + 8(v/4) + 4(l/32) + v%4
+//   m:    running max (log2 domain, >= 0), lsum: this half-wave's partial sum
+//   vis:  keys < vis[qs] are visible to this lane's column
+template <typename T, int D, int KP, int VP, int NKB, int QSUB>
+__device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *Vt, int kv_row0,
+                                            int j_abs0, const uint4 (&qf)[QSUB][D / 16],
+                                            f32x16_t (&oacc)[QSUB][D / 32], float (&m)[QSUB],
+                                            float (&lsum)[QSUB], bool need_mask,
+                                            const int (&vis)[QSUB], float scale_log2) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 5, r32 = lane & 31;
+    f32x16_t s[NKB][QSUB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int qs = 0; qs < QSUB; ++qs)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) s[kb][qs][v] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            const uint4 a = *reinterpret_cast<const uint4 *>(
+                Ks + (kv_row0 + 32 * kb + r32) * KP + 16 * ks + 8 * g);
+#pragma unroll
+            for (int qs = 0; qs < QSUB; ++qs) s[kb][qs] = Mma<T>::run(a, qf[qs][ks], s[kb][qs]);
+        }
+    }
+    uint4 pf[2 * NKB][QSUB];
+#pragma unroll
+    for (int qs = 0; qs < QSUB; ++qs) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                float x = s[kb][qs][v] * scale_log2;
+                if (need_mask) {
+                    const int kv = j_abs0 + 32 * kb + 8 * (v >> 2) + 4 * g + (v & 3);
+                    if (kv >= vis[qs]) x = kNegInf;
+                }
+                s[kb][qs][v] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m[qs], mx);  // m[qs] >= 0 keeps the reference clamp
+        const float alpha = __builtin_amdgcn_exp2f(m[qs] - m_new);
+        float sum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float e = __builtin_amdgcn_exp2f(s[kb][qs][v] - m_new);
+                s[kb][qs][v] = e;
+                sum += e;
+            }
+        lsum[qs] = lsum[qs] * alpha + sum;
+        m[qs] = m_new;
+        if (!__all(alpha == 1.0f)) {
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) oacc[qs][db][v] *= alpha;
+        }
+#pragma unroll
+        for (int t = 0; t < 2 * NKB; ++t) {
+            const int kb = t >> 1, o = 8 * (t & 1);
+            pf[t][qs].x = Mma<T>::pack2(s[kb][qs][o + 0], s[kb][qs][o + 1]);
+            pf[t][qs].y = Mma<T>::pack2(s[kb][qs][o + 2], s[kb][qs][o + 3]);
+            pf[t][qs].z = Mma<T>::pack2(s[kb][qs][o + 4], s[kb][qs][o + 5]);
+            pf[t][qs].w = Mma<T>::pack2(s[kb][qs][o + 6], s[kb][qs][o + 7]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 2 * NKB; ++t) {
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+            const uint16_t *vr = Vt + (32 * db + r32) * VP + kv_row0 + 16 * t + 4 * g;
+            const uint2 lo2 = *reinterpret_cast<const uint2 *>(vr);
+            const uint2 hi2 = *reinterpret_cast<const uint2 *>(vr + 8);
+            const uint4 a = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
+#pragma unroll
+            for (int qs = 0; qs < QSUB; ++qs) oacc[qs][db] = Mma<T>::run(a, pf[t][qs], oacc[qs][db]);
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store_row4(uint16_t *dst, float a, float b, float c, float d) {
+    uint2 w;
+    w.x = Mma<T>::pack2(a, b);
+    w.y = Mma<T>::pack2(c, d);
+    *reinterpret_cast<uint2 *>(dst) = w;
+}
+
+// ---------------------------------------------------------------- prefill
+
+template <typename T, int D, int HW, int QSUB>
+__global__ void __launch_bounds__(256) fa_prefill_kernel(FaParams p) {
+    constexpr int TILE = 64, NKB = 2;
+    using Loader = TileLoader<D, TILE, 256>;
+    constexpr int KP = Loader::KP, VP = Loader::VP;
+    constexpr int WROWS = 32 * QSUB;
+    constexpr int QT = WROWS * (4 / HW);
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[TILE * KP];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VP];
+
+    int bx = blockIdx.x;
+    const int ngroups = p.G / HW;
+    const int hg = bx % ngroups;
+    bx /= ngroups;
+    const int kvh = bx % p.Hkv;
+    const int b = bx / p.Hkv;
+    const int tile = gridDim.y - 1 - blockIdx.y;  // heaviest causal tiles first
+    long long q_off;
+    int L;
+    seq_info(p, b, q_off, L);
+    const int q0 = tile * QT;
+    if (q0 >= L) return;
+    const int S = p.kv_lens[b];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 5, r32 = lane & 31;
+    const int h = kvh * p.G + hg * HW + (wave % HW);
+    const int qw0 = q0 + (wave / HW) * WROWS;
+    const int q_start = p.causal ? max(S - L, 0) : 0;
+    const int last_row = min(q0 + QT, L) - 1;
+    const int kv_end = p.causal ? min(S, q_start + last_row + 1) : S;
+    const int *bt_row = p.bt + b * p.bt_stride;
+
+    uint4 qf[QSUB][D / 16];
+    int vis[QSUB];
+#pragma unroll
+    for (int qs = 0; qs < QSUB; ++qs) {
+        const int row = qw0 + 32 * qs + r32;
+        const uint16_t *src = p.q + ((q_off + row) * p.H + h) * D;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks)
+            qf[qs][ks] = row < L ? *reinterpret_cast<const uint4 *>(src + 16 * ks + 8 * g)
+                                 : make_uint4(0, 0, 0, 0);
+        vis[qs] = p.causal ? min(S, q_start + row + 1) : S;
+    }
+    const int wave_min_vis = p.causal ? min(S, q_start + qw0 + 1) : S;
+
+    float m[QSUB], lsum[QSUB];
+    f32x16_t oacc[QSUB][D / 32];
+#pragma unroll
+    for (int qs = 0; qs < QSUB; ++qs) {
+        m[qs] = 0.0f;
+        lsum[qs] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) oacc[qs][db][v] = 0.0f;
+    }
+
+    Loader ld;
+    const int ntiles = (kv_end + TILE - 1) / TILE;
+    if (ntiles > 0) ld.load(p, bt_row, kvh, 0, S);
+    for (int it = 0; it < ntiles; ++it) {
+        const int j0 = it * TILE;
+        __syncthreads();
+        ld.store(Ks, Vt);
+        __syncthreads();
+        if (it + 1 < ntiles) ld.load(p, bt_row, kvh, j0 + TILE, S);
+        const bool need_mask = j0 + TILE > wave_min_vis;
+        wave_attend<T, D, KP, VP, NKB, QSUB>(Ks, Vt, 0, j0, qf, oacc, m, lsum, need_mask, vis,
+                                             p.scale_log2);
+    }
+
+#pragma unroll
+    for (int qs = 0; qs < QSUB; ++qs) {
+        const float lt = lsum[qs] + __shfl_xor(lsum[qs], 32, 64);
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        const int row = qw0 + 32 * qs + r32;
+        if (row < L) {
+            uint16_t *dst = p.o + ((q_off + row) * p.H + h) * D;
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    store_row4<T>(dst + 32 * db + 8 * u + 4 * g, oacc[qs][db][4 * u] * inv,
+                                  oacc[qs][db][4 * u + 1] * inv, oacc[qs][db][4 * u + 2] * inv,
+                                  oacc[qs][db][4 * u + 3] * inv);
+        }
+    }
+}
+
+// ----------------------------------------------------------------- decode
+
+constexpr int kDecTile = 128;
+
+template <int D>
+constexpr size_t decode_lds_bytes() {
+    return sizeof(uint16_t) * (kDecTile * (D + 8) + D * (kDecTile + 4));
+}
+
+// Workgroup (b, kv head, split): keys [split*split_len, +split_len).  Column c
+// of the MFMA tile is (head c / rq, row c % rq) of the GQA group.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) fa_decode_kernel(FaParams p) {
+    using Loader = TileLoader<D, kDecTile, 256>;
+    constexpr int KP = Loader::KP, VP = Loader::VP;
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    uint16_t *Ks = smem;
+    uint16_t *Vt = smem + kDecTile * KP;
+
+    const int kvh = blockIdx.x % p.Hkv;
+    const int b = blockIdx.x / p.Hkv;
+    const int split = blockIdx.y;
+    long long q_off;
+    int L;
+    seq_info(p, b, q_off, L);
+    if (L <= 0) return;
+    const int S = p.kv_lens[b];
+    const int kv_lo = split * p.split_len;
+    if (split > 0 && kv_lo >= S) return;
+    const int kv_hi = min(S, kv_lo + p.split_len);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 5, r32 = lane & 31;
+    const int hl = r32 / p.rq, row = r32 % p.rq;
+    const bool col_ok = hl < p.G && row < L;
+    const int h = kvh * p.G + hl;
+    const int q_start = p.causal ? max(S - L, 0) : 0;
+    const int *bt_row = p.bt + b * p.bt_stride;
+
+    uint4 qf[1][D / 16];
+    int vis[1];
+    {
+        const uint16_t *src = p.q + ((q_off + row) * p.H + h) * D;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks)
+            qf[0][ks] = col_ok ? *reinterpret_cast<const uint4 *>(src + 16 * ks + 8 * g)
+                               : make_uint4(0, 0, 0, 0);
+        vis[0] = min(kv_hi, p.causal ? q_start + row + 1 : S);
+    }
+    const int min_vis = min(kv_hi, p.causal ? q_start + 1 : S);
+
+    float m[1] = {0.0f}, lsum[1] = {0.0f};
+    f32x16_t oacc[1][D / 32];
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) oacc[0][db][v] = 0.0f;
+
+    Loader ld;
+    const int ntiles = (kv_hi - kv_lo + kDecTile - 1) / kDecTile;
+    if (ntiles > 0) ld.load(p, bt_row, kvh, kv_lo, kv_hi);
+    for (int it = 0; it < ntiles; ++it) {
+        const int j0 = kv_lo + it * kDecTile;
+        __syncthreads();
+        ld.store(Ks, Vt);
+        __syncthreads();
+        if (it + 1 < ntiles) ld.load(p, bt_row, kvh, j0 + kDecTile, kv_hi);
+        const int jw = j0 + 32 * wave;
+        const bool need_mask = jw + 32 > min_vis;
+        wave_attend<T, D, KP, VP, 1, 1>(Ks, Vt, 32 * wave, jw, qf, oacc, m, lsum, need_mask, vis,
+                                        p.scale_log2);
+    }
+
+    // Merge the 4 waves' partial states in LDS (reusing the tile buffers).
+    __syncthreads();
+    float *lm = reinterpret_cast<float *>(smem);   // [4][32] max
+    float *ll = lm + 4 * 32;                        // [4][32] sum
+    float *lo = ll + 4 * 32;                        // [4][32][D] unnormalised O
+    const float lt = lsum[0] + __shfl_xor(lsum[0], 32, 64);
+    if (g == 0) {
+        lm[wave * 32 + r32] = m[0];
+        ll[wave * 32 + r32] = lt;
+    }
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int d = 32 * db + 8 * (v >> 2) + 4 * g + (v & 3);
+            lo[(wave * 32 + r32) * D + d] = oacc[0][db][v];
+        }
+    __syncthreads();
+    const long long base = (static_cast<long long>(b) * p.Hkv + kvh) * p.max_splits + split;
+    for (int task = threadIdx.x; task < p.ncols * D; task += blockDim.x) {
+        const int c = task / D, d = task % D;
+        float M = lm[c];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) M = fmaxf(M, lm[w * 32 + c]);
+        float acc = 0.0f, lsum_all = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float f = __builtin_amdgcn_exp2f(lm[w * 32 + c] - M);
+            acc += f * lo[(w * 32 + c) * D + d];
+            lsum_all += f * ll[w * 32 + c];
+        }
+        p.ws_o[(base * p.ncols + c) * D + d] = acc;
+        if (d == 0) {
+            p.ws_ml[(base * p.ncols + c) * 2] = M;
+            p.ws_ml[(base * p.ncols + c) * 2 + 1] = lsum_all;
+        }
+    }
+}
+
+// Merges the split partials of (b, kv head) into the output rows.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) fa_decode_combine_kernel(FaParams p) {
+    const int kvh = blockIdx.x % p.Hkv;
+    const int b = blockIdx.x / p.Hkv;
+    long long q_off;
+    int L;
+    seq_info(p, b, q_off, L);
+    if (L <= 0) return;
+    const int S = p.kv_lens[b];
+    int nsplit = S <= 0 ? 1 : (S + p.split_len - 1) / p.split_len;
+    nsplit = min(nsplit, p.max_splits);
+    const long long base = (static_cast<long long>(b) * p.Hkv + kvh) * p.max_splits;
+    for (int task = threadIdx.x; task < p.ncols * D; task += blockDim.x) {
+        const int c = task / D, d = task % D;
+        const int hl = c / p.rq, row = c % p.rq;
+        if (hl >= p.G || row >= L) continue;
+        float M = 0.0f;
+        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.ws_ml[((base + s) * p.ncols + c) * 2]);
+        float acc = 0.0f, l = 0.0f;
+        for (int s = 0; s < nsplit; ++s) {
+            const float f = __builtin_amdgcn_exp2f(p.ws_ml[((base + s) * p.ncols + c) * 2] - M);
+            acc += f * p.ws_o[((base + s) * p.ncols + c) * D + d];
+            l += f * p.ws_ml[((base + s) * p.ncols + c) * 2 + 1];
+        }
+        const float out = l > 0.0f ? acc / l : 0.0f;
+        const int h = kvh * p.G + hl;
+        p.o[((q_off + row) * p.H + h) * D + d] = Cvt<T>::from(out);
+    }
+}
+
+// ------------------------------------------------------------------- host
+
+struct Plan {
+    bool decode;
+    int rq, ncols, split_len, max_splits;
+};
+
+Plan make_plan(int batch, int H, int Hkv, int max_q, int max_k) {
+    Plan pl{};
+    const int G = H / Hkv;
+    pl.decode = max_q >= 1 && G * max_q <= 32;
+    pl.rq = max_q;
+    pl.ncols = G * max_q;
+    // Split the key range so that the grid has at least ~2048 workgroups.
+    const long long units = static_cast<long long>(batch) * Hkv;
+    int split = 512;
+    while (split > kDecTile && units * ((max_k + split - 1) / split) < 2048) split >>= 1;
+    pl.split_len = split;
+    pl.max_splits = max_k <= 0 ? 1 : (max_k + split - 1) / split;
+    return pl;
+}
+
+size_t workspace_bytes(const Plan &pl, int batch, int Hkv, int D) {
+    if (!pl.decode) return 0;
+    const size_t per = static_cast<size_t>(batch) * Hkv * pl.max_splits * pl.ncols;
+    return per * D * sizeof(float) + per * 2 * sizeof(float) + 256;
+}
+
+template <typename T, int D>
+tecoopsStatus_t run(tecoopsHandle_t handle, FaParams &p, const Plan &pl, int max_q) {
+    hipStream_t s = handle->stream;
+    if (pl.decode) {
+        const size_t lds = decode_lds_bytes<D>();
+        static bool attr_set = false;  // per template instance
+        if (!attr_set) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void *>(&fa_decode_kernel<T, D>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(lds)) != hipSuccess) {
+                (void)hipGetLastError();
+                TECO_ERROR("flash_attention: cannot reserve %zu bytes of LDS", lds);
+                return TECOOPS_STATUS_INTERNAL_ERROR;
+            }
+            attr_set = true;
+        }
+        dim3 grid(p.batch * p.Hkv, pl.max_splits);
+        hipLaunchKernelGGL((fa_decode_kernel<T, D>), grid, dim3(256), lds, s, p);
+        TECO_CHECK_LAUNCH("flash_attention decode");
+        hipLaunchKernelGGL((fa_decode_combine_kernel<T, D>), dim3(p.batch * p.Hkv), dim3(256), 0,
+                           s, p);
+        TECO_CHECK_LAUNCH("flash_attention combine");
+        return TECOOPS_STATUS_SUCCESS;
+    }
+    const int G = p.G;
+    const int HW = (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1);
+    constexpr int QSUB = 1;
+    const int QT = 32 * QSUB * (4 / HW);
+    dim3 grid(p.batch * p.Hkv * (G / HW), (max_q + QT - 1) / QT);
+    switch (HW) {
+        case 4: hipLaunchKernelGGL((fa_prefill_kernel<T, D, 4, QSUB>), grid, dim3(256), 0, s, p); break;
+        case 2: hipLaunchKernelGGL((fa_prefill_kernel<T, D, 2, QSUB>), grid, dim3(256), 0, s, p); break;
+        default: hipLaunchKernelGGL((fa_prefill_kernel<T, D, 1, QSUB>), grid, dim3(256), 0, s, p); break;
+    }
+    TECO_CHECK_LAUNCH("flash_attention prefill");
+    return TECOOPS_STATUS_SUCCESS;
+}
+
+bool is_packed_rowmajor(const tecoopsTensorStruct *d) {
+    int expect = 1;
+    for (int i = d->nbDims - 1; i >= 0; --i) {
+        if (d->dimA[i] > 1 && d->strideA[i] != expect) return false;
+        expect *= d->dimA[i];
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" tecoopsStatus_t tecoopsGetFlashAttentionWorkspaceSize(int batch, int num_heads,
+                                                                 int head_size, int max_seqlen_q,
+                                                                 int max_seqlen_k, size_t *bytes) {
+    if (bytes == nullptr || batch <= 0 || num_heads <= 0 || head_size <= 0 || max_seqlen_q <= 0 ||
+        max_seqlen_k < 0)
+        return TECOOPS_STATUS_BAD_PARAM;
+    // Worst case over kv-head counts: ncols * Hkv = H * max_q columns per split.
+    size_t worst = 0;
+    for (int hkv = 1; hkv <= num_heads; ++hkv) {
+        if (num_heads % hkv) continue;
+        const Plan pl = make_plan(batch, num_heads, hkv, max_seqlen_q, max_seqlen_k);
+        const size_t b = workspace_bytes(pl, batch, hkv, head_size);
+        if (b > worst) worst = b;
+    }
+    *bytes = worst;
+    return TECOOPS_STATUS_SUCCESS;
+}
+
+extern "C" tecoopsStatus_t tecoopsFlashAttentionEx(
+    tecoopsHandle_t handle, int max_seqlen_q, int max_seqlen_k, const int *q_seq_lens,
+    const int *cu_seqlens_q, const int *kv_seq_lens, const tecoopsTensorDescriptor_t btDesc,
+    const void *blockTable, const tecoopsTensorDescriptor_t qDesc, const void *qData,
+    const tecoopsTensorDescriptor_t kDesc, const void *kCache,
+    const tecoopsTensorDescriptor_t vDesc, const void *vCache,
+    const tecoopsTensorDescriptor_t oDesc, void *oData, float softmax_scale, int causal,
+    void *workspace) {
+    // Checks of reference flash_attention.cpp:44-69, extended to bf16 and to
+    // the shape facts the kernels rely on.
+    if (handle == nullptr) return TECOOPS_STATUS_NOT_INITIALIZED;
+    if (!btDesc || !qDesc || !kDesc || !vDesc || !oDesc) return TECOOPS_STATUS_BAD_PARAM;
+    if (!blockTable || !qData || !kCache || !vCache || !oData || !kv_seq_lens)
+        return TECOOPS_STATUS_BAD_PARAM;
+    if (q_seq_lens == nullptr && cu_seqlens_q == nullptr) return TECOOPS_STATUS_BAD_PARAM;
+    TECO_RETURN_IF(kDesc->dataType != vDesc->dataType, TECOOPS_STATUS_BAD_PARAM,
+                   "k_cache data_type must be equal to v_cache data_type");
+    TECO_RETURN_IF(!tecoops::is_16bit_float(kDesc->dataType), TECOOPS_STATUS_BAD_PARAM,
+                   "k/v cache must be TECOOPS_DATA_HALF or TECOOPS_DATA_BFLOAT16");
+    TECO_RETURN_IF(qDesc->dataType != kDesc->dataType || oDesc->dataType != kDesc->dataType,
+                   TECOOPS_STATUS_BAD_PARAM, "q, k/v cache and output types must agree");
+    TECO_RETURN_IF(kDesc->nbDims != 4 || vDesc->nbDims != 4 || qDesc->nbDims != 3 ||
+                   oDesc->nbDims != 3 || btDesc->nbDims != 2,
+                   TECOOPS_STATUS_BAD_PARAM, "flash_attention: unexpected tensor ranks");
+    for (int i = 0; i < 4; ++i)
+        TECO_RETURN_IF(kDesc->dimA[i] != vDesc->dimA[i], TECOOPS_STATUS_BAD_PARAM,
+                       "shape of k v cache is not equal");
+    for (int i = 0; i < 3; ++i)
+        TECO_RETURN_IF(qDesc->dimA[i] != oDesc->dimA[i], TECOOPS_STATUS_BAD_PARAM,
+                       "q and output shapes differ");
+    const int H = qDesc->dimA[1], D = qDesc->dimA[2];
+    const int num_blocks = kDesc->dimA[0], Hkv = kDesc->dimA[1], bs = kDesc->dimA[2];
+    const int batch = btDesc->dimA[0];
+    TECO_RETURN_IF(kDesc->dimA[3] != D, TECOOPS_STATUS_BAD_PARAM, "head_size mismatch");
+    TECO_RETURN_IF(D != 64 && D != 128, TECOOPS_STATUS_NOT_SUPPORTED,
+                   "flash_attention: head_size %d not supported (64, 128)", D);
+    TECO_RETURN_IF(H <= 0 || Hkv <= 0 || H % Hkv != 0, TECOOPS_STATUS_BAD_PARAM,
+                   "num_heads must be a multiple of num_kv_heads");
+    TECO_RETURN_IF(bs <= 0 || num_blocks <= 0 || batch <= 0, TECOOPS_STATUS_BAD_PARAM,
+                   "empty cache or batch");
+    TECO_RETURN_IF(max_seqlen_q <= 0 || max_seqlen_k < 0, TECOOPS_STATUS_BAD_PARAM,
+                   "max_seqlen_q must be > 0 and max_seqlen_k >= 0");
+    TECO_RETURN_IF(!is_packed_rowmajor(qDesc) || !is_packed_rowmajor(oDesc) ||
+                   !is_packed_rowmajor(kDesc) || !is_packed_rowmajor(vDesc) ||
+                   btDesc->strideA[1] != 1,
+                   TECOOPS_STATUS_NOT_SUPPORTED, "flash_attention: tensors must be row-major");
+    for (const void *ptr : {qData, kCache, vCache, static_cast<const void *>(oData)})
+        TECO_RETURN_IF(!tecoops::aligned(ptr, 16), TECOOPS_STATUS_BAD_PARAM,
+                       "flash_attention: tensors must be 16-byte aligned");
+
+    FaParams p{};
+    p.q = static_cast<const uint16_t *>(qData);
+    p.kc = static_cast<const uint16_t *>(kCache);
+    p.vc = static_cast<const uint16_t *>(vCache);
+    p.o = static_cast<uint16_t *>(oData);
+    p.bt = static_cast<const int *>(blockTable);
+    p.bt_stride = btDesc->strideA[0];
+    p.q_lens = q_seq_lens;
+    p.cu_q = cu_seqlens_q;
+    p.kv_lens = kv_seq_lens;
+    p.batch = batch;
+    p.H = H;
+    p.Hkv = Hkv;
+    p.G = H / Hkv;
+    p.bs = bs;
+    p.num_blocks = num_blocks;
+    const float scale = softmax_scale > 0.0f ? softmax_scale : 1.0f / std::sqrt(static_cast<float>(D));
+    p.scale_log2 = scale * 1.4426950408889634f;
+    p.causal = causal != 0;
+
+    const Plan pl = make_plan(batch, H, Hkv, max_seqlen_q, max_seqlen_k);
+    if (pl.decode) {
+        p.rq = pl.rq;
+        p.ncols = pl.ncols;
+        p.split_len = pl.split_len;
+        p.max_splits = pl.max_splits;
+        const size_t need = workspace_bytes(pl, batch, Hkv, D);
+        void *ws = workspace;
+        if (ws == nullptr) {
+            tecoopsStatus_t st = tecoops::handle_scratch(handle, need, &ws);
+            if (st != TECOOPS_STATUS_SUCCESS) return st;
+        }
+        const size_t per = static_cast<size_t>(batch) * Hkv * pl.max_splits * pl.ncols;
+        p.ws_o = static_cast<float *>(ws);
+        p.ws_ml = p.ws_o + per * D;
+    }
+    using tecoops::dev::bf16;
+    using tecoops::dev::f16;
+    if (kDesc->dataType == TECOOPS_DATA_BFLOAT16)
+        return D == 128 ? run<bf16, 128>(handle, p, pl, max_seqlen_q)
+                        : run<bf16, 64>(handle, p, pl, max_seqlen_q);
+    return D == 128 ? run<f16, 128>(handle, p, pl, max_seqlen_q)
+                    : run<f16, 64>(handle, p, pl, max_seqlen_q);
+}
+
+extern "C" tecoopsStatus_t tecoopsFlashAttention(
+    tecoopsHandle_t handle, int max_seqlen_q, int max_seqlen_k, int max_block_num,
+    const int *q_seq_lens, const int *kv_seq_lens, const tecoopsTensorDescriptor_t blockTableDesc,
+    const void *blockTable, const tecoopsTensorDescriptor_t qDataDesc, const void *qData,
+    const tecoopsTensorDescriptor_t kCacheDesc, const void *kCache,
+    const tecoopsTensorDescriptor_t vCacheDesc, const void *vCache,
+    const tecoopsTensorDescriptor_t oDataDesc, void *oData, void *workspace) {
+    (void)max_block_num;  // the reference also takes the block count from kCacheDesc
+    if (q_seq_lens == nullptr) return handle ? TECOOPS_STATUS_BAD_PARAM : TECOOPS_STATUS_NOT_INITIALIZED;
+    return tecoopsFlashAttentionEx(handle, max_seqlen_q, max_seqlen_k, q_seq_lens, nullptr,
+                                   kv_seq_lens, blockTableDesc, blockTable, qDataDesc, qData,
+                                   kCacheDesc, kCache, vCacheDesc, vCache, oDataDesc, oData,
+                                   -1.0f, 1, workspace);
+}

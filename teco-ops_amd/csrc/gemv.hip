@@ -1,0 +1,307 @@
+// gemv.hip — decode-time matrix-vector products that stream the weight
+// matrix at HBM rate.
+//
+// No reference implementation: GEMV is absent from the reference library.
+//   fp16 / bf16:  y[b, n] = T( sum_k W[n, k] * x[b, k] )            fp32 acc
+//   int8:         y[b, n] = fp16( s[n] * sum_k float(Wq[n, k]) * x[b, k] )
+//
+// gfx950 design: a workgroup of 4 waves owns 4*R consecutive output rows and
+// first stages x ([B, K], at most 64 KiB) in LDS.  Each wave streams R rows of
+// W with 16-byte loads, lane-interleaved along K so that every load
+// instruction reads a contiguous 1 KiB run of a row, and keeps R x B fp32
+// partial sums; the products use v_dot2_f32_{f16,bf16} (two MACs per
+// instruction, fp32 accumulation).  int8 weights are widened exactly to fp16
+// with one v_perm_b32 (bytes of w+128 under the exponent of 1024.0) and one
+// packed fp16 subtract of 1152 per weight pair.  A wave-wide xor-shuffle
+// reduction finishes each (row, batch) sum; the per-row int8 scale is applied
+// to the fp32 sum.  HBM-bound: algorithmic bytes = |W| + |x| + |y| (+|s|).
+#include "common.h"
+#include "device.h"
+
+namespace {
+
+using namespace tecoops::dev;
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+template <typename T> struct Dot2;
+template <> struct Dot2<f16> {
+    static __device__ __forceinline__ float run(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a),
+                                      __builtin_bit_cast(half2_t, b), c, false);
+    }
+};
+template <> struct Dot2<bf16> {
+    static __device__ __forceinline__ float run(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf162_t, a),
+                                               __builtin_bit_cast(bf162_t, b), c, false);
+    }
+};
+
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// Streaming 16-byte load of weight data that is read exactly once.
+__device__ __forceinline__ uint4 load_stream(const uint4 *p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Copies x [B, K] (16-bit elements, K % 8 == 0) into LDS.
+__device__ __forceinline__ void stage_x(uint4 *xs, const uint4 *x, int nvec) {
+    for (int i = threadIdx.x; i < nvec; i += blockDim.x) xs[i] = x[i];
+    __syncthreads();
+}
+
+template <typename T, int B, int R>
+__global__ void __launch_bounds__(kThreads)
+gemv16_kernel(const uint4 *__restrict__ W, const uint4 *__restrict__ x, uint16_t *__restrict__ y,
+              int N, int K) {
+    extern __shared__ uint4 xs[];
+    const int kv = K / 8;  // 16-byte chunks per row
+    stage_x(xs, x, B * kv);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * kWaves + wave) * R;
+    if (n0 >= N) return;
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
+    const uint4 *wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kv;
+#pragma unroll 2
+    for (int c = lane; c < kv; c += 64) {
+        uint4 wv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) wv[r] = load_stream(wrow[r] + c);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const uint4 xv = xs[b * kv + c];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float s = acc[r][b];
+                s = Dot2<T>::run(wv[r].x, xv.x, s);
+                s = Dot2<T>::run(wv[r].y, xv.y, s);
+                s = Dot2<T>::run(wv[r].z, xv.z, s);
+                s = Dot2<T>::run(wv[r].w, xv.w, s);
+                acc[r][b] = s;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float s = wave_sum(acc[r][b]);
+            if (lane == 0 && n0 + r < N) y[static_cast<long long>(b) * N + n0 + r] = Cvt<T>::from(s);
+        }
+}
+
+// int8 weight dword (4 values) -> two packed fp16 pairs holding the exact values.
+__device__ __forceinline__ void widen_i8(uint32_t w, uint32_t &p01, uint32_t &p23) {
+    const uint32_t u = w ^ 0x80808080u;  // bytes now hold w + 128 in [0, 255]
+    const half2_t bias = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    // 0x64XX as fp16 is 1024 + XX
+    half2_t h01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
+    half2_t h23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
+    p01 = __builtin_bit_cast(uint32_t, h01 + bias);
+    p23 = __builtin_bit_cast(uint32_t, h23 + bias);
+}
+
+template <int B, int R>
+__global__ void __launch_bounds__(kThreads)
+gemv_i8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
+               const uint4 *__restrict__ x, uint16_t *__restrict__ y, int N, int K) {
+    extern __shared__ uint4 xs[];
+    const int kx = K / 8;    // 16-byte chunks of an x row (8 fp16)
+    const int kw = K / 16;   // 16-byte chunks of a W row (16 int8)
+    stage_x(xs, x, B * kx);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * kWaves + wave) * R;
+    if (n0 >= N) return;
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
+    const uint4 *wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kw;
+#pragma unroll 2
+    for (int c = lane; c < kw; c += 64) {
+        uint32_t wh[R][8];  // 16 weights as 8 fp16 pairs
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint4 q = load_stream(wrow[r] + c);
+            widen_i8(q.x, wh[r][0], wh[r][1]);
+            widen_i8(q.y, wh[r][2], wh[r][3]);
+            widen_i8(q.z, wh[r][4], wh[r][5]);
+            widen_i8(q.w, wh[r][6], wh[r][7]);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const uint4 x0 = xs[b * kx + 2 * c];
+            const uint4 x1 = xs[b * kx + 2 * c + 1];
+            const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float s = acc[r][b];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) s = Dot2<f16>::run(wh[r][j], xv[j], s);
+                acc[r][b] = s;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float sc = (n0 + r < N) ? h2f(scales[n0 + r]) : 0.0f;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float s = wave_sum(acc[r][b]);
+            if (lane == 0 && n0 + r < N) y[static_cast<long long>(b) * N + n0 + r] = f2h(sc * s);
+        }
+    }
+}
+
+// Fallback for shapes the vector kernels do not take (K not a multiple of 8 /
+// 16, misaligned pointers): one wave per (row, batch), element-wise.
+template <typename T, bool INT8>
+__global__ void __launch_bounds__(kThreads)
+gemv_scalar_kernel(const void *__restrict__ Wv, const uint16_t *__restrict__ scales,
+                   const uint16_t *__restrict__ x, uint16_t *__restrict__ y, int N, int K,
+                   int batch) {
+    const int lane = threadIdx.x & 63;
+    const long long task = static_cast<long long>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (task >= static_cast<long long>(N) * batch) return;
+    const int n = static_cast<int>(task % N), b = static_cast<int>(task / N);
+    float s = 0.0f;
+    for (int k = lane; k < K; k += 64) {
+        const float w = INT8 ? static_cast<float>(static_cast<const int8_t *>(Wv)[static_cast<long long>(n) * K + k])
+                             : Cvt<T>::to(static_cast<const uint16_t *>(Wv)[static_cast<long long>(n) * K + k]);
+        s += w * Cvt<T>::to(x[static_cast<long long>(b) * K + k]);
+    }
+    s = wave_sum(s);
+    if (lane == 0) {
+        if (INT8) s *= h2f(scales[n]);
+        y[static_cast<long long>(b) * N + n] = Cvt<T>::from(s);
+    }
+}
+
+constexpr int kMaxLdsBytes = 64 * 1024;
+
+template <typename T, int B>
+void launch16(const void *W, const void *x, void *y, int N, int K, hipStream_t s) {
+    constexpr int R = 4;
+    const unsigned grid = tecoops::ceil_div(N, kWaves * R);
+    hipLaunchKernelGGL((gemv16_kernel<T, B, R>), dim3(grid), dim3(kThreads), B * K * 2, s,
+                       static_cast<const uint4 *>(W), static_cast<const uint4 *>(x),
+                       static_cast<uint16_t *>(y), N, K);
+}
+
+template <int B>
+void launch_i8(const void *W, const void *sc, const void *x, void *y, int N, int K,
+               hipStream_t s) {
+    constexpr int R = 4;
+    const unsigned grid = tecoops::ceil_div(N, kWaves * R);
+    hipLaunchKernelGGL((gemv_i8_kernel<B, R>), dim3(grid), dim3(kThreads), B * K * 2, s,
+                       static_cast<const uint4 *>(W), static_cast<const uint16_t *>(sc),
+                       static_cast<const uint4 *>(x), static_cast<uint16_t *>(y), N, K);
+}
+
+template <typename T>
+void launch16_b(int B, const void *W, const void *x, void *y, int N, int K, hipStream_t s) {
+    switch (B) {
+        case 1: launch16<T, 1>(W, x, y, N, K, s); break;
+        case 2: launch16<T, 2>(W, x, y, N, K, s); break;
+        case 3: launch16<T, 3>(W, x, y, N, K, s); break;
+        case 4: launch16<T, 4>(W, x, y, N, K, s); break;
+        case 5: launch16<T, 5>(W, x, y, N, K, s); break;
+        case 6: launch16<T, 6>(W, x, y, N, K, s); break;
+        case 7: launch16<T, 7>(W, x, y, N, K, s); break;
+        default: launch16<T, 8>(W, x, y, N, K, s); break;
+    }
+}
+
+void launch_i8_b(int B, const void *W, const void *sc, const void *x, void *y, int N, int K,
+                 hipStream_t s) {
+    switch (B) {
+        case 1: launch_i8<1>(W, sc, x, y, N, K, s); break;
+        case 2: launch_i8<2>(W, sc, x, y, N, K, s); break;
+        case 3: launch_i8<3>(W, sc, x, y, N, K, s); break;
+        case 4: launch_i8<4>(W, sc, x, y, N, K, s); break;
+        case 5: launch_i8<5>(W, sc, x, y, N, K, s); break;
+        case 6: launch_i8<6>(W, sc, x, y, N, K, s); break;
+        case 7: launch_i8<7>(W, sc, x, y, N, K, s); break;
+        default: launch_i8<8>(W, sc, x, y, N, K, s); break;
+    }
+}
+
+}  // namespace
+
+extern "C" tecoopsStatus_t tecoopsGemv(tecoopsHandle_t handle, const void *weight, const void *x,
+                                       void *y, int batch, int n, int k,
+                                       tecoopsDataType_t dataType) {
+    if (handle == nullptr) return TECOOPS_STATUS_NOT_INITIALIZED;
+    if (weight == nullptr || x == nullptr || y == nullptr) return TECOOPS_STATUS_BAD_PARAM;
+    if (batch <= 0 || n <= 0 || k <= 0) return TECOOPS_STATUS_BAD_PARAM;
+    if (!tecoops::is_16bit_float(dataType)) return TECOOPS_STATUS_BAD_PARAM;
+    using tecoops::dev::bf16;
+    using tecoops::dev::f16;
+    hipStream_t s = handle->stream;
+    const bool vec = (k % 8) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16) &&
+                     8 * k * 2 <= kMaxLdsBytes;
+    if (vec) {
+        // Batches beyond 8 run in slices of 8 rows of x / y.
+        for (int b0 = 0; b0 < batch; b0 += 8) {
+            const int nb = batch - b0 < 8 ? batch - b0 : 8;
+            const void *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
+            void *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
+            if (dataType == TECOOPS_DATA_HALF) launch16_b<f16>(nb, weight, xb, yb, n, k, s);
+            else launch16_b<bf16>(nb, weight, xb, yb, n, k, s);
+            TECO_CHECK_LAUNCH("gemv");
+        }
+        return TECOOPS_STATUS_SUCCESS;
+    }
+    const unsigned grid = tecoops::ceil_div(static_cast<long long>(n) * batch, kWaves);
+    if (dataType == TECOOPS_DATA_HALF)
+        hipLaunchKernelGGL((gemv_scalar_kernel<f16, false>), dim3(grid), dim3(kThreads), 0, s,
+                           weight, nullptr, static_cast<const uint16_t *>(x),
+                           static_cast<uint16_t *>(y), n, k, batch);
+    else
+        hipLaunchKernelGGL((gemv_scalar_kernel<bf16, false>), dim3(grid), dim3(kThreads), 0, s,
+                           weight, nullptr, static_cast<const uint16_t *>(x),
+                           static_cast<uint16_t *>(y), n, k, batch);
+    TECO_CHECK_LAUNCH("gemv");
+    return TECOOPS_STATUS_SUCCESS;
+}
+
+extern "C" tecoopsStatus_t tecoopsGemvInt8(tecoopsHandle_t handle, const int8_t *weight,
+                                           const void *scales, const void *x, void *y,
+                                           int batch, int n, int k) {
+    if (handle == nullptr) return TECOOPS_STATUS_NOT_INITIALIZED;
+    if (weight == nullptr || scales == nullptr || x == nullptr || y == nullptr)
+        return TECOOPS_STATUS_BAD_PARAM;
+    if (batch <= 0 || n <= 0 || k <= 0) return TECOOPS_STATUS_BAD_PARAM;
+    using tecoops::dev::f16;
+    hipStream_t s = handle->stream;
+    const bool vec = (k % 16) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16) &&
+                     8 * k * 2 <= kMaxLdsBytes;
+    if (vec) {
+        for (int b0 = 0; b0 < batch; b0 += 8) {
+            const int nb = batch - b0 < 8 ? batch - b0 : 8;
+            const void *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
+            void *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
+            launch_i8_b(nb, weight, scales, xb, yb, n, k, s);
+            TECO_CHECK_LAUNCH("gemv_int8");
+        }
+        return TECOOPS_STATUS_SUCCESS;
+    }
+    const unsigned grid = tecoops::ceil_div(static_cast<long long>(n) * batch, kWaves);
+    hipLaunchKernelGGL((gemv_scalar_kernel<f16, true>), dim3(grid), dim3(kThreads), 0, s,
+                       static_cast<const void *>(weight), static_cast<const uint16_t *>(scales),
+                       static_cast<const uint16_t *>(x), static_cast<uint16_t *>(y), n, k, batch);
+    TECO_CHECK_LAUNCH("gemv_int8");
+    return TECOOPS_STATUS_SUCCESS;
+}

@@ -1,0 +1,150 @@
+"""GPU parity of flash attention (prefill and split-KV decode) against the
+CPU oracle (flash_attention.py:79-140 restated in oracle/oracle.c).
+
+Tolerance 1e-2 abs/rel as the north star states (the reference's own python
+tests use max-abs < 2e-2, python_api_test/test_flash_attention.py:167).  The
+DIFF1 criterion of the reference C++ cases (sum|d| / sum|b| <= 1e-2,
+flash_attention/test_case/*.prototxt test_param) is asserted as well.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import tecoops
+from oracle import oracle as orc
+
+from helpers import as_f32, assert_close, bits, dev, reference_cases
+
+pytestmark = pytest.mark.gpu
+
+CASES = reference_cases()["flash_attention"]
+
+
+def make_inputs(seed, H, Hkv, D, BS, q_lens, kv_lens, num_blocks=None, dtype=orc.HALF,
+                shuffle=True):
+    r = np.random.default_rng(seed)
+    need = sum(-(-s // BS) for s in kv_lens)
+    NB = max(num_blocks or 0, need)
+    kc = bits(r.uniform(-1, 1, (NB, Hkv, BS, D)), dtype)
+    vc = bits(r.uniform(-1, 1, (NB, Hkv, BS, D)), dtype)
+    q = bits(r.uniform(-1, 1, (sum(q_lens), H, D)), dtype)
+    ids = r.permutation(NB) if shuffle else np.arange(NB)
+    cols = max(1, max(-(-s // BS) for s in kv_lens))
+    # entries past each sequence's last block hold garbage ids on purpose
+    bt = r.integers(-5, 10 * NB, (len(kv_lens), cols)).astype(np.int32)
+    i = 0
+    for b, s in enumerate(kv_lens):
+        for j in range(-(-s // BS)):
+            bt[b, j] = ids[i]
+            i += 1
+    return q, kc, vc, bt
+
+
+def run_gpu(q, kc, vc, bt, q_lens, kv_lens, dtype=orc.HALF, scale=None, causal=True):
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    out = torch.empty(q.shape, dtype=torch.float16 if dtype == orc.HALF else torch.bfloat16,
+                      device="cuda")
+    D = q.shape[2]
+    tecoops.flash_attn_varlen_func(dev(q, dtype), dev(kc, dtype), dev(vc, dtype), max(q_lens),
+                                   dev(cu), max(kv_lens), None, dev(np.array(kv_lens, np.int32)),
+                                   scale if scale else 1.0 / math.sqrt(D), causal, None, dev(bt),
+                                   False, out)
+    torch.cuda.synchronize()
+    return as_f32(out, dtype)
+
+
+def check(case, dtype=orc.HALF, seed=0, causal=True):
+    q, kc, vc, bt = make_inputs(seed, case["H"], case["Hkv"], case["D"], case["bs"],
+                                case["q_lens"], case["kv_lens"], case.get("num_blocks"), dtype)
+    got = run_gpu(q, kc, vc, bt, case["q_lens"], case["kv_lens"], dtype, causal=causal)
+    ref = orc.flash_attention(q, kc, vc, bt, case["q_lens"], case["kv_lens"], causal=causal,
+                              dtype=dtype)
+    assert_close(got, ref, what=case["name"])
+    diff1 = np.abs(got - ref).sum() / max(np.abs(ref).sum(), 1e-30)
+    assert diff1 <= 1e-2, diff1
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: c["name"])
+def test_reference_cases_fp16(case):
+    check(case, orc.HALF, seed=1)
+
+
+@pytest.mark.parametrize("case", CASES[:5], ids=lambda c: c["name"])
+def test_reference_cases_bf16(case):
+    check(case, orc.BF16, seed=2)
+
+
+@pytest.mark.parametrize("bs", [16, 1, 5, 64])
+def test_block_sizes(bs):
+    case = dict(name=f"bs{bs}", H=8, Hkv=2, D=128, bs=bs, q_lens=[1, 70, 129],
+                kv_lens=[200, 70, 300])
+    check(case, orc.BF16, seed=bs)
+
+
+def test_non_causal_and_chunk_longer_than_kv():
+    case = dict(name="noncausal", H=4, Hkv=4, D=64, bs=16, q_lens=[33, 5], kv_lens=[40, 100])
+    check(case, orc.HALF, seed=3, causal=False)
+    # q_len > kv_len: the kernel's q_start clamp (flash_attention.scpp:75-76)
+    case = dict(name="q_gt_kv", H=4, Hkv=2, D=128, bs=16, q_lens=[50], kv_lens=[20])
+    check(case, orc.HALF, seed=4)
+
+
+def test_empty_kv_gives_zero_rows():
+    case = dict(name="empty", H=4, Hkv=1, D=128, bs=16, q_lens=[1, 3], kv_lens=[0, 0])
+    q, kc, vc, bt = make_inputs(5, 4, 1, 128, 16, [1, 3], [1, 1])
+    got = run_gpu(q, kc, vc, bt, case["q_lens"], [0, 0])
+    assert not got.any()
+
+
+def test_decode_gqa_and_speculative_rows():
+    # G * q_len <= 32 takes the split-KV decode path
+    for H, Hkv, ql in ((32, 8, 1), (16, 2, 4), (8, 1, 1), (32, 1, 1)):
+        case = dict(name=f"dec{H}/{Hkv}x{ql}", H=H, Hkv=Hkv, D=128, bs=16,
+                    q_lens=[ql] * 5, kv_lens=[1, 17, 600, 2049, 3000])
+        check(case, orc.BF16, seed=H + ql)
+
+
+def test_softmax_scale_honoured():
+    q, kc, vc, bt = make_inputs(6, 4, 2, 64, 16, [10], [30])
+    got = run_gpu(q, kc, vc, bt, [10], [30], scale=0.3)
+    ref = orc.flash_attention(q, kc, vc, bt, [10], [30], softmax_scale=0.3)
+    assert_close(got, ref, what="scale 0.3")
+
+
+def test_baseline_decode_config():
+    """BASELINE decode: bf16, B=64, 32 heads / 8 kv heads, D=128, 1 query token
+    per sequence, paged cache of block 16 with shuffled block ids, seeded
+    context lengths U{512..8192}."""
+    r = np.random.default_rng(2025)
+    kv = r.integers(512, 8193, 64).tolist()
+    q, kc, vc, bt = make_inputs(11, 32, 8, 128, 16, [1] * 64, kv, dtype=orc.BF16)
+    got = run_gpu(q, kc, vc, bt, [1] * 64, kv, orc.BF16)
+    ref = orc.flash_attention(q, kc, vc, bt, [1] * 64, kv, dtype=orc.BF16)
+    assert_close(got, ref, what="decode B=64")
+
+
+def test_prefill_medium_bf16():
+    case = dict(name="prefill1k", H=32, Hkv=8, D=128, bs=16, q_lens=[1024], kv_lens=[1024])
+    check(case, orc.BF16, seed=12)
+
+
+def test_baseline_prefill_config_sampled_heads():
+    """BASELINE prefill: bf16 q [4, 32, 4096, 128], GQA k/v [4, 8, 4096, 128],
+    causal.  The whole output is checked for finiteness and for the causal
+    structure (row 0 of every head equals V row 0); one head of the last
+    sequence is checked against the oracle in full."""
+    B, H, Hkv, D, S = 4, 32, 8, 128, 4096
+    q, kc, vc, bt = make_inputs(13, H, Hkv, D, 16, [S] * B, [S] * B, dtype=orc.BF16,
+                                shuffle=False)
+    got = run_gpu(q, kc, vc, bt, [S] * B, [S] * B, orc.BF16)
+    assert np.isfinite(got).all()
+    v = orc.to_float(vc, orc.BF16)
+    for b in range(B):
+        v0 = v[bt[b, 0], :, 0]  # [Hkv, D]
+        assert_close(got[b * S], np.repeat(v0, H // Hkv, axis=0), what=f"row0 b{b}")
+    ref = orc.flash_attention(q, kc, vc, bt, [S] * B, [S] * B, dtype=orc.BF16, b_only=B - 1,
+                              h_begin=H - 1, h_end=H)
+    sl = slice((B - 1) * S, B * S)
+    assert_close(got[sl, H - 1], ref[sl, H - 1], what="prefill b3 h31")

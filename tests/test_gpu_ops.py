@@ -1,0 +1,310 @@
+"""GPU parity of the bandwidth-bound ops against the CPU oracle.
+
+Each test calls libtecoops.so through the C ABI (tecoops package) on cuda:0
+with seeded inputs and compares with oracle/oracle.c on the same inputs:
+bit-exact for reshape_and_cache and memset, within 1e-2 abs/rel for the
+fp16/bf16 ops, 1e-2 relative for the int8 GEMV.  Shapes: the reference's own
+test cases (tests/golden/reference_cases.json), edge cases, and the full
+BASELINE.json configs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import tecoops
+from oracle import oracle as orc
+
+from helpers import as_f32, assert_close, bits, dev, host_bits, reference_cases
+
+pytestmark = pytest.mark.gpu
+
+CASES = reference_cases()
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ------------------------------------------------------------- reshape_and_cache
+
+def _run_reshape(T, H, D, NB, BS, seed, dtype=orc.HALF, neg=0, collisions_free=True,
+                 out_of_range=0):
+    r = rng(seed)
+    key = bits(r.standard_normal((T, H, D)), dtype)
+    value = bits(r.standard_normal((T, H, D)), dtype)
+    slots = r.permutation(NB * BS)[:T].astype(np.int64)
+    if neg:
+        slots[r.choice(T, neg, replace=False)] = -1
+    if out_of_range:
+        slots[r.choice(T, out_of_range, replace=False)] = NB * BS + 5
+    sentinel = bits(np.full((NB, H, BS, D), 3.5), dtype)
+    kc_ref, vc_ref = sentinel.copy(), sentinel.copy()
+    orc.reshape_and_cache(key, value, slots, kc_ref, vc_ref)
+    kc, vc = dev(sentinel, dtype), dev(sentinel, dtype)
+    tecoops.reshape_and_cache(dev(key, dtype), dev(value, dtype), dev(slots), kc, vc)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(kc), kc_ref)
+    assert np.array_equal(host_bits(vc), vc_ref)
+
+
+@pytest.mark.parametrize("case", CASES["reshape_and_cache"], ids=lambda c: f"kv{c['kv_heads']}")
+def test_reshape_and_cache_reference_cases(case):
+    _run_reshape(case["tokens"], case["kv_heads"], case["head"], case["num_blocks"],
+                 case["block_size"], seed=42, neg=7)
+
+
+@pytest.mark.parametrize("D", [6, 7, 64])
+def test_reshape_and_cache_narrow_heads_and_bf16(D):
+    _run_reshape(100, 3, D, 20, 8, seed=D, dtype=orc.BF16, neg=3, out_of_range=2)
+
+
+def test_reshape_and_cache_baseline_config():
+    """BASELINE config: 8192 tokens x 8 kv heads x 128, 1024 blocks x 16,
+    slot_mapping a seeded permutation of distinct slots in [0, 16384)."""
+    _run_reshape(8192, 8, 128, 1024, 16, seed=1234)
+
+
+# ---------------------------------------------------------------------- rms_norm
+
+def _run_rms(N, D, eps, residual, seed, dtype=orc.HALF):
+    r = rng(seed)
+    x = bits(r.uniform(-1, 1, (N, D)), dtype)
+    w = bits(r.uniform(0.5, 1.5, D), dtype)
+    res = bits(r.uniform(-1, 1, (N, D)), dtype) if residual else None
+    ref, ref_res = orc.rms_norm(x, w, residual=res, eps=eps, dtype=dtype)
+    tdt = torch.float16 if dtype == orc.HALF else torch.bfloat16
+    out = torch.empty((N, D), dtype=tdt, device="cuda")
+    res_out = torch.empty((N, D), dtype=tdt, device="cuda") if residual else None
+    tecoops.rms_norm(dev(x, dtype), dev(w, dtype), dev(res, dtype) if residual else None, out,
+                     res_out, eps)
+    torch.cuda.synchronize()
+    assert_close(as_f32(out, dtype), orc.to_float(ref, dtype), what="rms_norm out")
+    if residual:
+        assert np.array_equal(host_bits(res_out), ref_res)
+
+
+@pytest.mark.parametrize("case", CASES["rms_norm"],
+                         ids=lambda c: f"{c['hidden']}-{'add' if c['residual'] else 'pure'}")
+def test_rms_norm_reference_cases(case):
+    _run_rms(case["tokens"], case["hidden"], case["eps"], case["residual"], seed=42)
+
+
+@pytest.mark.parametrize("D", [100, 8, 24576, 20000])
+def test_rms_norm_odd_and_wide_rows(D):
+    _run_rms(5, D, 1e-5, residual=True, seed=D)
+    _run_rms(5, D, 1e-5, residual=False, seed=D + 1)
+
+
+def test_rms_norm_bf16():
+    _run_rms(33, 2048, 1e-6, residual=True, seed=7, dtype=orc.BF16)
+
+
+def test_rms_norm_baseline_config():
+    """BASELINE config: x fp16 [4096, 4096] ~N(0,1), w ~U(0.5,1.5), eps 1e-6."""
+    r = rng(2024)
+    x = bits(r.standard_normal((4096, 4096)))
+    w = bits(r.uniform(0.5, 1.5, 4096))
+    ref, _ = orc.rms_norm(x, w, eps=1e-6)
+    out = torch.empty((4096, 4096), dtype=torch.float16, device="cuda")
+    tecoops.rms_norm(dev(x), dev(w), None, out, None, 1e-6)
+    torch.cuda.synchronize()
+    got = host_bits(out)
+    assert_close(orc.to_float(got), orc.to_float(ref), what="rms_norm 4096^2")
+    # fp32 sums in a different order: at most 1 ulp of fp16 from the oracle
+    ulp = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+    assert ulp.max() <= 1
+
+
+# ------------------------------------------------------------------------ rotary
+
+def _run_rotary(T, H, Hkv, D, seed, is_neox=True, use_cache=False, dtype=orc.HALF,
+                rot_dim=None, maxpos=2048):
+    r = rng(seed)
+    q = bits(r.standard_normal((T, H, D)), dtype)
+    k = bits(r.standard_normal((T, Hkv, D)), dtype)
+    pos = (np.arange(T) % maxpos).astype(np.int64)
+    r.shuffle(pos)
+    rd = rot_dim or D
+    cache = None
+    if use_cache:
+        i = np.arange(rd // 2)
+        th = np.arange(maxpos)[:, None] * 10000.0 ** (-2 * i / rd)
+        cache = np.concatenate([np.cos(th), np.sin(th)], 1).astype(np.float32)
+    qo, ko = orc.rotary_embedding(pos, q, k, rot_dim=rd, is_neox=is_neox, cos_sin_cache=cache,
+                                  dtype=dtype)
+    qt, kt = dev(q, dtype), dev(k, dtype)
+    tecoops.rotary_embedding(dev(pos), qt, kt, D, dev(cache) if use_cache else None,
+                             is_neox=is_neox, rot_dim=rd)
+    torch.cuda.synchronize()
+    assert_close(as_f32(qt, dtype), qo, what="rotary q")
+    assert_close(as_f32(kt, dtype), ko, what="rotary k")
+
+
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("use_cache", [False, True])
+def test_rotary_variants(is_neox, use_cache):
+    _run_rotary(300, 4, 2, 128, seed=5, is_neox=is_neox, use_cache=use_cache)
+
+
+def test_rotary_partial_rot_dim_bf16_and_scalar_path():
+    _run_rotary(64, 3, 1, 64, seed=6, rot_dim=32, dtype=orc.BF16)
+    _run_rotary(64, 3, 1, 20, seed=7, rot_dim=10)   # rot/2 = 5: scalar path
+
+
+def test_rotary_baseline_config():
+    """BASELINE config: q [8192, 32, 128], k [8192, 8, 128], positions 0..2047
+    per sequence, base 10000, neox."""
+    r = rng(99)
+    T = 8192
+    q = bits(r.standard_normal((T, 32, 128)))
+    k = bits(r.standard_normal((T, 8, 128)))
+    pos = (np.arange(T) % 2048).astype(np.int64)
+    qo, ko = orc.rotary_embedding(pos, q, k)
+    qt, kt = dev(q), dev(k)
+    tecoops.rotary_embedding(dev(pos), qt, kt, 128)
+    torch.cuda.synchronize()
+    assert_close(as_f32(qt), qo, what="rotary q")
+    assert_close(as_f32(kt), ko, what="rotary k")
+
+
+# ------------------------------------------------------------------ causal_conv1d
+
+@pytest.mark.parametrize("ci", range(len(CASES["causal_conv1d"])))
+def test_causal_conv1d_reference_cases(ci):
+    """Reference torch layout: x/out [dim, tokens], weight [width, dim]
+    (python_api_test/test_causal_conv1d.py:108-147)."""
+    c = CASES["causal_conv1d"][ci]
+    r = rng(100 + ci)
+    dim, lens = c["dim"], c["seq_lens"]
+    total = sum(lens)
+    x = bits(r.standard_normal((dim, total)))
+    w = bits(r.standard_normal((4, dim)))
+    st = bits(r.standard_normal((c["num_entries"], 3, dim)))
+    qsl = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cidx = np.array(c["cache_indices"], np.int32)
+    hinit = np.array(c["has_init"], np.int8)
+    st_ref = st.copy()
+    ref = orc.causal_conv1d(x, w, conv_state=st_ref, query_start_loc=qsl, cache_indices=cidx,
+                            has_initial_state=hinit, pad_slot_id=c["pad_slot_id"], layout="dl")
+    out = torch.zeros((dim, total), dtype=torch.float16, device="cuda")
+    st_dev = dev(st)
+    tecoops.causal_conv1d_fn_torch(out, st_dev, dev(x), dev(w), dev(qsl), dev(cidx), dev(hinit),
+                                   c["pad_slot_id"])
+    torch.cuda.synchronize()
+    assert_close(as_f32(out), ref, what="conv out")
+    assert np.array_equal(host_bits(st_dev), st_ref)
+
+
+def test_causal_conv1d_c_api_token_major():
+    """tecoopsCausalConv1d with the reference C layout [tokens, dim], api_mode 1
+    and width 3 / 2 (state of width-1 rows)."""
+    import ctypes
+    from tecoops import _lib
+    for W in (4, 3, 2):
+        r = rng(200 + W)
+        dim, lens = 96, [5, 1, 2, 40]
+        total = sum(lens)
+        x = bits(r.standard_normal((total, dim)))
+        w = bits(r.standard_normal((W, dim)))
+        st = bits(r.standard_normal((len(lens), W - 1, dim)))
+        qsl = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        st_ref = st.copy()
+        ref = orc.causal_conv1d(x, w, conv_state=st_ref, query_start_loc=qsl, api_mode=1,
+                                layout="ld")
+        xd, wd, sd, qd = dev(x), dev(w), dev(st), dev(qsl)
+        out = torch.zeros((total, dim), dtype=torch.float16, device="cuda")
+        h = ctypes.c_void_p()
+        _lib.call("tecoopsCreate", ctypes.byref(h))
+        _lib.call("tecoopsSetStream", h, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        _lib.call("tecoopsCausalConv1d", h, len(lens), total, dim, W, (W - 1) * dim, dim, dim,
+                  -1, 1, 0, ctypes.c_void_p(xd.data_ptr()), ctypes.c_void_p(sd.data_ptr()),
+                  ctypes.c_void_p(wd.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                  ctypes.c_void_p(qd.data_ptr()), None, None)
+        torch.cuda.synchronize()
+        _lib.call("tecoopsDestroy", h)
+        assert_close(as_f32(out), ref, what=f"conv width {W}")
+        assert np.array_equal(host_bits(sd), st_ref)
+
+
+def test_causal_conv1d_baseline_config():
+    """BASELINE config: x fp16 [8, 4096, 2048] ~N(0,1), weight [4096, 4]
+    ~N(0,0.5), bias [4096] ~N(0,1), SiLU, final state written."""
+    r = rng(77)
+    B, dim, L = 8, 4096, 2048
+    x = bits(r.standard_normal((B, dim, L)))
+    w = bits(r.normal(0, 0.5, (dim, 4)))
+    bias = bits(r.standard_normal(dim))
+    st = np.zeros((B, 3, dim), np.uint16)
+    ref = orc.causal_conv1d(x, w, bias=bias, conv_state=st, layout="bdl")
+    out = torch.empty((B, dim, L), dtype=torch.float16, device="cuda")
+    st_dev = torch.zeros((B, 3, dim), dtype=torch.float16, device="cuda")
+    tecoops.causal_conv1d(dev(x), dev(w), dev(bias), out, conv_states=st_dev)
+    torch.cuda.synchronize()
+    assert_close(as_f32(out), ref, what="conv 8x4096x2048")
+    assert np.array_equal(host_bits(st_dev), st)
+
+
+# -------------------------------------------------------------------------- GEMV
+
+@pytest.mark.parametrize("B", [1, 8, 3, 11])
+def test_gemv_fp16(B):
+    r = rng(300 + B)
+    N, K = (14336, 4096) if B in (1, 8) else (1000, 512)
+    W = bits(r.normal(0, 0.02, (N, K)))
+    x = bits(r.standard_normal((B, K)))
+    ref = orc.gemv(W, x)
+    y = torch.empty((B, N), dtype=torch.float16, device="cuda")
+    tecoops.gemv(dev(W), dev(x), y)
+    torch.cuda.synchronize()
+    assert_close(as_f32(y), ref, what=f"gemv B={B}")
+
+
+@pytest.mark.parametrize("B", [1, 8, 5])
+def test_gemv_int8(B):
+    r = rng(400 + B)
+    N, K = (14336, 4096) if B in (1, 8) else (777, 1024)
+    W = r.integers(-127, 128, (N, K), dtype=np.int8)
+    s = bits(r.uniform(0.001, 0.01, N))
+    x = bits(r.standard_normal((B, K)))
+    ref = orc.gemv_int8(W, s, x)
+    y = torch.empty((B, N), dtype=torch.float16, device="cuda")
+    tecoops.gemv_int8(dev(W), dev(s), dev(x), y)
+    torch.cuda.synchronize()
+    got = as_f32(y)
+    # 1e-2 relative, with an absolute floor of 1e-3 of the output scale for
+    # outputs that cancel to near zero
+    assert_close(got, ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2, what=f"gemv_int8 B={B}")
+
+
+def test_gemv_odd_shapes_and_bf16():
+    r = rng(500)
+    for N, K, dt in ((33, 100, orc.HALF), (64, 4096, orc.BF16)):
+        W = bits(r.normal(0, 0.05, (N, K)), dt)
+        x = bits(r.standard_normal((2, K)), dt)
+        ref = orc.gemv(W, x, dtype=dt)
+        y = torch.empty((2, N), dtype=torch.float16 if dt == orc.HALF else torch.bfloat16,
+                        device="cuda")
+        tecoops.gemv(dev(W, dt), dev(x, dt), y)
+        torch.cuda.synchronize()
+        assert_close(as_f32(y, dt), ref, what=f"gemv {N}x{K}")
+    W = r.integers(-127, 128, (50, 40), dtype=np.int8)  # K % 16 != 0: scalar path
+    s = bits(r.uniform(0.001, 0.01, 50))
+    x = bits(r.standard_normal((1, 40)))
+    y = torch.empty((1, 50), dtype=torch.float16, device="cuda")
+    tecoops.gemv_int8(dev(W), dev(s), dev(x), y)
+    torch.cuda.synchronize()
+    assert_close(as_f32(y), orc.gemv_int8(W, s, x), what="gemv_int8 scalar")
+
+
+# ------------------------------------------------------------------------ memset
+
+@pytest.mark.parametrize("offset,size", [(0, 4096), (3, 1000), (1, 15), (5, 1 << 20)])
+def test_memset_bit_exact(offset, size):
+    buf = torch.full((size + 64,), 0x11, dtype=torch.uint8, device="cuda")
+    view = buf[offset:offset + size]
+    tecoops.memset(view, 0x3a7)
+    torch.cuda.synchronize()
+    h = buf.cpu().numpy()
+    ref = np.full(size + 64, 0x11, np.uint8)
+    orc.memset(ref[offset:offset + size], 0x3a7)
+    assert np.array_equal(h, ref)
