@@ -37,6 +37,10 @@
 //     then by a combine kernel.  HBM-bound: every cached K/V byte is read
 //     once.
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+#include <vector>
 
 #include "common.h"
 #include "device.h"
@@ -49,10 +53,12 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 template <typename T> struct Mma;
 template <> struct Mma<bf16> {
-    static __device__ __forceinline__ f32x16_t run(const uint4 &a, const uint4 &b, f32x16_t c) {
+    static __device__ __forceinline__ f32x16_t run(const u32x4 &a, const u32x4 &b, f32x16_t c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                        __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
     }
@@ -62,7 +68,7 @@ template <> struct Mma<bf16> {
     }
 };
 template <> struct Mma<f16> {
-    static __device__ __forceinline__ f32x16_t run(const uint4 &a, const uint4 &b, f32x16_t c) {
+    static __device__ __forceinline__ f32x16_t run(const u32x4 &a, const u32x4 &b, f32x16_t c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
                                                       __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
     }
@@ -84,7 +90,8 @@ struct FaParams {
     const int *q_lens;   // per-sequence q lengths, or NULL
     const int *cu_q;     // cumulative q offsets [batch+1], used when q_lens is NULL
     const int *kv_lens;
-    int batch, H, Hkv, G, bs, num_blocks;
+    int batch, H, Hkv, G, bs, lbs, num_blocks;  // lbs = log2(bs) when bs is a power of 2
+    long long page_stride;                      // Hkv * bs * D elements per cache block
     float scale_log2;    // softmax_scale * log2(e)
     int causal;
     // split-KV decode
@@ -92,6 +99,12 @@ struct FaParams {
     float *ws_ml;        // [B][Hkv][max_splits][ncols][2]
     int split_len, max_splits, rq, ncols;
 };
+
+// P values are computed against a running max that is only raised when a
+// tile's max exceeds it by more than this (log2 domain), so that the O / l
+// rescale runs rarely; P <= 2^kRescaleSlack stays exact in fp32 and keeps
+// its relative precision in 16 bit.
+constexpr float kRescaleSlack = 8.0f;
 
 __device__ __forceinline__ void seq_info(const FaParams &p, int b, long long &q_off, int &L) {
     if (p.q_lens == nullptr) {
@@ -105,100 +118,134 @@ __device__ __forceinline__ void seq_info(const FaParams &p, int b, long long &q_
     }
 }
 
-// Address of key row `kv` of kv head `kvh` of sequence b in a paged cache, or
-// nullptr when the row is beyond `kv_limit` or its page id is out of range.
-template <int D>
-__device__ __forceinline__ const uint16_t *kv_row(const FaParams &p, const uint16_t *cache,
-                                                  const int *bt_row, int kvh, int kv,
-                                                  int kv_limit) {
-    if (kv >= kv_limit) return nullptr;
-    const int page = bt_row[kv / p.bs];
-    if (page < 0 || page >= p.num_blocks) return nullptr;
-    return cache + ((static_cast<long long>(page) * p.Hkv + kvh) * p.bs + kv % p.bs) * D;
+// Element offset of key row `kv` of the (sequence, kv head) whose block-table
+// row is bt_row and whose head offset inside a block is head_off.  Rows at or
+// beyond kv_limit, and rows whose page id is out of range, are redirected to
+// a row that exists and reported through ok = false; the caller zeroes V for
+// them and masks K.
+template <int D, bool POW2>
+__device__ __forceinline__ long long row_offset(const FaParams &p, const int *bt_row,
+                                                long long head_off, int kv, int kv_limit,
+                                                bool &ok) {
+    ok = kv < kv_limit;
+    const int kvs = ok ? kv : 0;
+    int blk, off;
+    if (POW2) {
+        blk = kvs >> p.lbs;
+        off = kvs & (p.bs - 1);
+    } else {
+        blk = kvs / p.bs;
+        off = kvs - blk * p.bs;
+    }
+    int page = bt_row[blk];
+    ok = ok && page >= 0 && page < p.num_blocks;
+    page = ok ? page : 0;
+    return static_cast<long long>(page) * p.page_stride + head_off + static_cast<long long>(off) * D;
 }
 
 // Cooperative global -> register -> LDS staging of one TILE-key K/V tile by NT
 // threads.  K is stored row-major [TILE][D + 8]; V transposed [D][TILE + 4].
-template <int D, int TILE, int NT>
+// Each thread owns one 16-byte column of K (rows r0, r0 + KRS, ...) and
+// VPT (4-row x 8-column) blocks of V.
+template <int D, int TILE, int NT, bool POW2>
 struct TileLoader {
     static constexpr int KP = D + 8;
     static constexpr int VP = TILE + 4;
-    static constexpr int KCH = TILE * (D / 8) / NT;                 // K chunks per thread
-    static constexpr int VTASKS = (TILE / 4) * (D / 8);            // 4 rows x 8 cols each
+    static constexpr int ELEMS = TILE * KP + D * VP;  // one K + V^T buffer
+    static constexpr int CPR = D / 8;                  // 16-byte chunks per row
+    static constexpr int KCH = TILE * CPR / NT;
+    static constexpr int KRS = NT / CPR;
+    static constexpr int VTASKS = (TILE / 4) * CPR;
     static constexpr int VPT = (VTASKS + NT - 1) / NT;
-    static_assert(TILE * (D / 8) % NT == 0, "K tile must split evenly");
-    uint4 k[KCH];
-    uint4 v[VPT][4];
+    static_assert(TILE * CPR % NT == 0 && NT % CPR == 0, "K tile must split evenly");
+    u32x4 k[KCH];
+    u32x4 v[VPT][4];
 
-    __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, int kvh, int j0,
-                                         int kv_limit) {
+    __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
+                                         int j0, int kv_limit) {
         const int tid = threadIdx.x;
+        const int col = tid % CPR, r0 = tid / CPR;
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
-            const int c = tid + i * NT;
-            const int row = c / (D / 8), col = c % (D / 8);
-            const uint16_t *src = kv_row<D>(p, p.kc, bt_row, kvh, j0 + row, kv_limit);
-            k[i] = src ? *reinterpret_cast<const uint4 *>(src + col * 8) : make_uint4(0, 0, 0, 0);
+            bool ok;
+            const long long o = row_offset<D, POW2>(p, bt_row, head_off, j0 + r0 + i * KRS,
+                                                    kv_limit, ok);
+            k[i] = *reinterpret_cast<const u32x4 *>(p.kc + o + col * 8);
         }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int task = tid + i * NT;
+            if (VTASKS % NT != 0 && task >= VTASKS) continue;
             const int rg = task % (TILE / 4), cg = task / (TILE / 4);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const uint16_t *src = task < VTASKS
-                    ? kv_row<D>(p, p.vc, bt_row, kvh, j0 + 4 * rg + r, kv_limit) : nullptr;
-                v[i][r] = src ? *reinterpret_cast<const uint4 *>(src + cg * 8)
-                              : make_uint4(0, 0, 0, 0);
+                bool ok;
+                const long long o = row_offset<D, POW2>(p, bt_row, head_off, j0 + 4 * rg + r,
+                                                        kv_limit, ok);
+                const u32x4 x = *reinterpret_cast<const u32x4 *>(p.vc + o + cg * 8);
+                const u32x4 zero = {0u, 0u, 0u, 0u};
+                v[i][r] = ok ? x : zero;
             }
         }
     }
 
-    __device__ __forceinline__ void store(uint16_t *Ks, uint16_t *Vt) const {
+    __device__ __forceinline__ void store(uint16_t *buf) const {
+        uint16_t *Ks = buf;
+        uint16_t *Vt = buf + TILE * KP;
         const int tid = threadIdx.x;
+        const int col = tid % CPR, r0 = tid / CPR;
 #pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = tid + i * NT;
-            const int row = c / (D / 8), col = c % (D / 8);
-            *reinterpret_cast<uint4 *>(Ks + row * KP + col * 8) = k[i];
-        }
+        for (int i = 0; i < KCH; ++i)
+            *reinterpret_cast<u32x4 *>(Ks + (r0 + i * KRS) * KP + col * 8) = k[i];
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int task = tid + i * NT;
-            if (task >= VTASKS) continue;
+            if (VTASKS % NT != 0 && task >= VTASKS) continue;
             const int rg = task % (TILE / 4), cg = task / (TILE / 4);
-            const uint32_t *r0 = reinterpret_cast<const uint32_t *>(&v[i][0]);
-            const uint32_t *r1 = reinterpret_cast<const uint32_t *>(&v[i][1]);
-            const uint32_t *r2 = reinterpret_cast<const uint32_t *>(&v[i][2]);
-            const uint32_t *r3 = reinterpret_cast<const uint32_t *>(&v[i][3]);
+            const u32x4 a = v[i][0], b = v[i][1], c = v[i][2], d = v[i][3];
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 // columns d = 8cg + 2w (low halves) and 8cg + 2w + 1 (high halves)
-                uint2 lo2, hi2;
-                lo2.x = (r0[w] & 0xffffu) | (r1[w] << 16);
-                lo2.y = (r2[w] & 0xffffu) | (r3[w] << 16);
-                hi2.x = (r0[w] >> 16) | (r1[w] & 0xffff0000u);
-                hi2.y = (r2[w] >> 16) | (r3[w] & 0xffff0000u);
-                *reinterpret_cast<uint2 *>(Vt + (8 * cg + 2 * w) * VP + 4 * rg) = lo2;
-                *reinterpret_cast<uint2 *>(Vt + (8 * cg + 2 * w + 1) * VP + 4 * rg) = hi2;
+                u32x2 lo2, hi2;
+                lo2.x = __builtin_amdgcn_perm(b[w], a[w], 0x05040100u);
+                lo2.y = __builtin_amdgcn_perm(d[w], c[w], 0x05040100u);
+                hi2.x = __builtin_amdgcn_perm(b[w], a[w], 0x07060302u);
+                hi2.y = __builtin_amdgcn_perm(d[w], c[w], 0x07060302u);
+                *reinterpret_cast<u32x2 *>(Vt + (8 * cg + 2 * w) * VP + 4 * rg) = lo2;
+                *reinterpret_cast<u32x2 *>(Vt + (8 * cg + 2 * w + 1) * VP + 4 * rg) = hi2;
             }
         }
     }
 };
 
+template <typename T> struct Ones2;
+template <> struct Ones2<bf16> {
+    static __device__ __forceinline__ float dot(uint32_t a, float c) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf162_t, a),
+                                               __builtin_bit_cast(bf162_t, 0x3f803f80u), c, false);
+    }
+};
+template <> struct Ones2<f16> {
+    static __device__ __forceinline__ float dot(uint32_t a, float c) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a),
+                                      __builtin_bit_cast(half2_t, 0x3c003c00u), c, false);
+    }
+};
+
 // One wave's online-softmax attention over NKB 32-key blocks staged in LDS at
-// rows [kv_row0, kv_row0 + 32*NKB), absolute key index j_abs0 for kv_row0.
-// Lane l owns query column (l % 32) of each of its QSUB column blocks.
+// rows [kv_row0, kv_row0 + 32*NKB).  Lane l owns query column (l % 32) of each
+// of its QSUB column blocks.
 //   qf:   Q^T B-operand fragments (8 x 16-bit per lane per 16-dim k-step)
 //   oacc: O^T accumulators, element v of block db is d = 32db + 8(v/4) + 4(l/32) + v%4
-//   m:    running max (log2 domain, >= 0), lsum: this half-wave's partial sum
-//   vis:  keys < vis[qs] are visible to this lane's column
-template <typename T, int D, int KP, int VP, int NKB, int QSUB>
+//   m:    running max (log2 domain, >= 0), lsum: this half-wave's partial sum of P
+//   lim:  key r (0-based in the staged rows, r = 32kb + 8(v/4) + 4(l/32) + v%4)
+//         is visible when r - 4(l/32) < lim[qs]
+template <typename T, int D, int KP, int VP, int NKB, int QSUB, bool MASK>
 __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *Vt, int kv_row0,
-                                            int j_abs0, const uint4 (&qf)[QSUB][D / 16],
+                                            const u32x4 (&qf)[QSUB][D / 16],
                                             f32x16_t (&oacc)[QSUB][D / 32], float (&m)[QSUB],
-                                            float (&lsum)[QSUB], bool need_mask,
-                                            const int (&vis)[QSUB], float scale_log2) {
+                                            float (&lsum)[QSUB], const int (&lim)[QSUB],
+                                            float scale_log2) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 5, r32 = lane & 31;
     f32x16_t s[NKB][QSUB];
@@ -212,13 +259,13 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-            const uint4 a = *reinterpret_cast<const uint4 *>(
+            const u32x4 a = *reinterpret_cast<const u32x4 *>(
                 Ks + (kv_row0 + 32 * kb + r32) * KP + 16 * ks + 8 * g);
 #pragma unroll
             for (int qs = 0; qs < QSUB; ++qs) s[kb][qs] = Mma<T>::run(a, qf[qs][ks], s[kb][qs]);
         }
     }
-    uint4 pf[2 * NKB][QSUB];
+    u32x4 pf[2 * NKB][QSUB];
 #pragma unroll
     for (int qs = 0; qs < QSUB; ++qs) {
         float mx = kNegInf;
@@ -226,34 +273,29 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                float x = s[kb][qs][v] * scale_log2;
-                if (need_mask) {
-                    const int kv = j_abs0 + 32 * kb + 8 * (v >> 2) + 4 * g + (v & 3);
-                    if (kv >= vis[qs]) x = kNegInf;
-                }
+                float x = s[kb][qs][v];
+                if (MASK && !(32 * kb + 8 * (v >> 2) + (v & 3) < lim[qs])) x = kNegInf;
                 s[kb][qs][v] = x;
                 mx = fmaxf(mx, x);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m[qs], mx);  // m[qs] >= 0 keeps the reference clamp
-        const float alpha = __builtin_amdgcn_exp2f(m[qs] - m_new);
-        float sum = 0.0f;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const float e = __builtin_amdgcn_exp2f(s[kb][qs][v] - m_new);
-                s[kb][qs][v] = e;
-                sum += e;
-            }
-        lsum[qs] = lsum[qs] * alpha + sum;
-        m[qs] = m_new;
-        if (!__all(alpha == 1.0f)) {
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+        if (!__all(mx <= m[qs] + kRescaleSlack)) {
+            const float m_new = fmaxf(m[qs], mx);  // m >= 0 keeps the reference clamp
+            const float alpha = __builtin_amdgcn_exp2f(m[qs] - m_new);
+            m[qs] = m_new;
+            lsum[qs] *= alpha;
 #pragma unroll
             for (int db = 0; db < D / 32; ++db)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) oacc[qs][db][v] *= alpha;
         }
+        const float mneg = -m[qs];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                s[kb][qs][v] = __builtin_amdgcn_exp2f(fmaf(s[kb][qs][v], scale_log2, mneg));
+        float l = lsum[qs];
 #pragma unroll
         for (int t = 0; t < 2 * NKB; ++t) {
             const int kb = t >> 1, o = 8 * (t & 1);
@@ -261,16 +303,21 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
             pf[t][qs].y = Mma<T>::pack2(s[kb][qs][o + 2], s[kb][qs][o + 3]);
             pf[t][qs].z = Mma<T>::pack2(s[kb][qs][o + 4], s[kb][qs][o + 5]);
             pf[t][qs].w = Mma<T>::pack2(s[kb][qs][o + 6], s[kb][qs][o + 7]);
+            l = Ones2<T>::dot(pf[t][qs].x, l);
+            l = Ones2<T>::dot(pf[t][qs].y, l);
+            l = Ones2<T>::dot(pf[t][qs].z, l);
+            l = Ones2<T>::dot(pf[t][qs].w, l);
         }
+        lsum[qs] = l;
     }
 #pragma unroll
     for (int t = 0; t < 2 * NKB; ++t) {
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) {
             const uint16_t *vr = Vt + (32 * db + r32) * VP + kv_row0 + 16 * t + 4 * g;
-            const uint2 lo2 = *reinterpret_cast<const uint2 *>(vr);
-            const uint2 hi2 = *reinterpret_cast<const uint2 *>(vr + 8);
-            const uint4 a = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
+            const u32x2 lo2 = *reinterpret_cast<const u32x2 *>(vr);
+            const u32x2 hi2 = *reinterpret_cast<const u32x2 *>(vr + 8);
+            const u32x4 a = {lo2.x, lo2.y, hi2.x, hi2.y};
 #pragma unroll
             for (int qs = 0; qs < QSUB; ++qs) oacc[qs][db] = Mma<T>::run(a, pf[t][qs], oacc[qs][db]);
         }
@@ -287,15 +334,25 @@ __device__ __forceinline__ void store_row4(uint16_t *dst, float a, float b, floa
 
 // ---------------------------------------------------------------- prefill
 
-template <typename T, int D, int HW, int QSUB>
-__global__ void __launch_bounds__(256) fa_prefill_kernel(FaParams p) {
-    constexpr int TILE = 64, NKB = 2;
-    using Loader = TileLoader<D, TILE, 256>;
+constexpr int kPreTile = 64;
+
+template <int D>
+constexpr size_t prefill_lds_bytes() {
+    return 2 * sizeof(uint16_t) * (kPreTile * (D + 8) + D * (kPreTile + 4));
+}
+
+// Workgroup (b, kv head, head group, query tile) with W waves: wave w serves
+// query head hg*HW + w % HW of the GQA group and query rows
+// [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of 64 keys are double
+// buffered in LDS: one barrier per tile.
+template <typename T, int D, int W, int HW, int QSUB, bool POW2>
+__global__ void __launch_bounds__(W * 64, QSUB == 1 ? 2 : 1) fa_prefill_kernel(FaParams p) {
+    constexpr int NT = W * 64, TILE = kPreTile, NKB = TILE / 32;
+    using Loader = TileLoader<D, TILE, NT, POW2>;
     constexpr int KP = Loader::KP, VP = Loader::VP;
     constexpr int WROWS = 32 * QSUB;
-    constexpr int QT = WROWS * (4 / HW);
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[TILE * KP];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VP];
+    constexpr int QT = WROWS * (W / HW);
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
 
     int bx = blockIdx.x;
     const int ngroups = p.G / HW;
@@ -315,23 +372,26 @@ __global__ void __launch_bounds__(256) fa_prefill_kernel(FaParams p) {
     const int h = kvh * p.G + hg * HW + (wave % HW);
     const int qw0 = q0 + (wave / HW) * WROWS;
     const int q_start = p.causal ? max(S - L, 0) : 0;
-    const int last_row = min(q0 + QT, L) - 1;
-    const int kv_end = p.causal ? min(S, q_start + last_row + 1) : S;
+    const int kv_end = p.causal ? min(S, q_start + min(q0 + QT, L)) : S;
+    const int wave_kv_end = p.causal ? min(S, q_start + min(qw0 + WROWS, L)) : S;
+    const int wave_min_vis = p.causal ? min(S, q_start + qw0 + 1) : S;
     const int *bt_row = p.bt + b * p.bt_stride;
+    const long long head_off = static_cast<long long>(kvh) * p.bs * D;
 
-    uint4 qf[QSUB][D / 16];
+    u32x4 qf[QSUB][D / 16];
     int vis[QSUB];
 #pragma unroll
     for (int qs = 0; qs < QSUB; ++qs) {
         const int row = qw0 + 32 * qs + r32;
-        const uint16_t *src = p.q + ((q_off + row) * p.H + h) * D;
+        const uint16_t *src = p.q + ((q_off + min(row, L - 1)) * p.H + h) * D;
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks)
-            qf[qs][ks] = row < L ? *reinterpret_cast<const uint4 *>(src + 16 * ks + 8 * g)
-                                 : make_uint4(0, 0, 0, 0);
+        for (int ks = 0; ks < D / 16; ++ks) {
+            const u32x4 x = *reinterpret_cast<const u32x4 *>(src + 16 * ks + 8 * g);
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            qf[qs][ks] = row < L ? x : zero;
+        }
         vis[qs] = p.causal ? min(S, q_start + row + 1) : S;
     }
-    const int wave_min_vis = p.causal ? min(S, q_start + qw0 + 1) : S;
 
     float m[QSUB], lsum[QSUB];
     f32x16_t oacc[QSUB][D / 32];
@@ -347,16 +407,28 @@ __global__ void __launch_bounds__(256) fa_prefill_kernel(FaParams p) {
 
     Loader ld;
     const int ntiles = (kv_end + TILE - 1) / TILE;
-    if (ntiles > 0) ld.load(p, bt_row, kvh, 0, S);
+    if (ntiles > 0) {
+        ld.load(p, bt_row, head_off, 0, S);
+        ld.store(lds);
+    }
+    __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
+        const uint16_t *cur = lds + (it & 1) * Loader::ELEMS;
+        if (it + 1 < ntiles) ld.load(p, bt_row, head_off, (it + 1) * TILE, S);
         const int j0 = it * TILE;
+        if (j0 < wave_kv_end) {
+            int lim[QSUB];
+#pragma unroll
+            for (int qs = 0; qs < QSUB; ++qs) lim[qs] = vis[qs] - j0 - 4 * g;
+            if (j0 + TILE > wave_min_vis)
+                wave_attend<T, D, KP, VP, NKB, QSUB, true>(cur, cur + TILE * KP, 0, qf, oacc, m,
+                                                           lsum, lim, p.scale_log2);
+            else
+                wave_attend<T, D, KP, VP, NKB, QSUB, false>(cur, cur + TILE * KP, 0, qf, oacc, m,
+                                                            lsum, lim, p.scale_log2);
+        }
+        if (it + 1 < ntiles) ld.store(lds + ((it + 1) & 1) * Loader::ELEMS);
         __syncthreads();
-        ld.store(Ks, Vt);
-        __syncthreads();
-        if (it + 1 < ntiles) ld.load(p, bt_row, kvh, j0 + TILE, S);
-        const bool need_mask = j0 + TILE > wave_min_vis;
-        wave_attend<T, D, KP, VP, NKB, QSUB>(Ks, Vt, 0, j0, qf, oacc, m, lsum, need_mask, vis,
-                                             p.scale_log2);
     }
 
 #pragma unroll
@@ -387,14 +459,13 @@ constexpr size_t decode_lds_bytes() {
 }
 
 // Workgroup (b, kv head, split): keys [split*split_len, +split_len).  Column c
-// of the MFMA tile is (head c / rq, row c % rq) of the GQA group.
-template <typename T, int D>
-__global__ void __launch_bounds__(256) fa_decode_kernel(FaParams p) {
-    using Loader = TileLoader<D, kDecTile, 256>;
+// of the MFMA tile is (head c / rq, row c % rq) of the GQA group; the 4 waves
+// take the four 32-key blocks of each 128-key tile.
+template <typename T, int D, bool POW2>
+__global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
+    using Loader = TileLoader<D, kDecTile, 256, POW2>;
     constexpr int KP = Loader::KP, VP = Loader::VP;
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    uint16_t *Ks = smem;
-    uint16_t *Vt = smem + kDecTile * KP;
 
     const int kvh = blockIdx.x % p.Hkv;
     const int b = blockIdx.x / p.Hkv;
@@ -411,20 +482,22 @@ __global__ void __launch_bounds__(256) fa_decode_kernel(FaParams p) {
     const int g = lane >> 5, r32 = lane & 31;
     const int hl = r32 / p.rq, row = r32 % p.rq;
     const bool col_ok = hl < p.G && row < L;
-    const int h = kvh * p.G + hl;
+    const int h = kvh * p.G + min(hl, p.G - 1);
     const int q_start = p.causal ? max(S - L, 0) : 0;
     const int *bt_row = p.bt + b * p.bt_stride;
+    const long long head_off = static_cast<long long>(kvh) * p.bs * D;
 
-    uint4 qf[1][D / 16];
-    int vis[1];
+    u32x4 qf[1][D / 16];
     {
-        const uint16_t *src = p.q + ((q_off + row) * p.H + h) * D;
+        const uint16_t *src = p.q + ((q_off + min(row, L - 1)) * p.H + h) * D;
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks)
-            qf[0][ks] = col_ok ? *reinterpret_cast<const uint4 *>(src + 16 * ks + 8 * g)
-                               : make_uint4(0, 0, 0, 0);
-        vis[0] = min(kv_hi, p.causal ? q_start + row + 1 : S);
+        for (int ks = 0; ks < D / 16; ++ks) {
+            const u32x4 x = *reinterpret_cast<const u32x4 *>(src + 16 * ks + 8 * g);
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            qf[0][ks] = col_ok ? x : zero;
+        }
     }
+    const int vis = min(kv_hi, p.causal ? q_start + row + 1 : S);
     const int min_vis = min(kv_hi, p.causal ? q_start + 1 : S);
 
     float m[1] = {0.0f}, lsum[1] = {0.0f};
@@ -436,17 +509,23 @@ __global__ void __launch_bounds__(256) fa_decode_kernel(FaParams p) {
 
     Loader ld;
     const int ntiles = (kv_hi - kv_lo + kDecTile - 1) / kDecTile;
-    if (ntiles > 0) ld.load(p, bt_row, kvh, kv_lo, kv_hi);
+    if (ntiles > 0) ld.load(p, bt_row, head_off, kv_lo, kv_hi);
     for (int it = 0; it < ntiles; ++it) {
         const int j0 = kv_lo + it * kDecTile;
         __syncthreads();
-        ld.store(Ks, Vt);
+        ld.store(smem);
         __syncthreads();
-        if (it + 1 < ntiles) ld.load(p, bt_row, kvh, j0 + kDecTile, kv_hi);
+        if (it + 1 < ntiles) ld.load(p, bt_row, head_off, j0 + kDecTile, kv_hi);
         const int jw = j0 + 32 * wave;
-        const bool need_mask = jw + 32 > min_vis;
-        wave_attend<T, D, KP, VP, 1, 1>(Ks, Vt, 32 * wave, jw, qf, oacc, m, lsum, need_mask, vis,
-                                        p.scale_log2);
+        if (jw < kv_hi) {
+            const int lim[1] = {vis - jw - 4 * g};
+            if (jw + 32 > min_vis)
+                wave_attend<T, D, KP, VP, 1, 1, true>(smem, smem + kDecTile * KP, 32 * wave, qf,
+                                                      oacc, m, lsum, lim, p.scale_log2);
+            else
+                wave_attend<T, D, KP, VP, 1, 1, false>(smem, smem + kDecTile * KP, 32 * wave, qf,
+                                                       oacc, m, lsum, lim, p.scale_log2);
+        }
     }
 
     // Merge the 4 waves' partial states in LDS (reusing the tile buffers).
@@ -547,42 +626,88 @@ size_t workspace_bytes(const Plan &pl, int batch, int Hkv, int D) {
     return per * D * sizeof(float) + per * 2 * sizeof(float) + 256;
 }
 
+// Raises a kernel's dynamic-LDS limit once per process (per kernel address).
+bool reserve_lds(const void *kernel, size_t bytes) {
+    static std::mutex mu;
+    static std::vector<const void *> done;
+    if (bytes <= 64 * 1024) return true;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const void *k : done)
+        if (k == kernel) return true;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(bytes)) != hipSuccess) {
+        (void)hipGetLastError();
+        TECO_ERROR("flash_attention: cannot reserve %zu bytes of LDS", bytes);
+        return false;
+    }
+    done.push_back(kernel);
+    return true;
+}
+
+// Prefill shapes: W waves per workgroup, QSUB 32-row query blocks per wave.
+// TECOOPS_FA_PREFILL="W,QSUB" selects one of (4,1), (8,1), (4,2) for tuning.
+struct PrefillCfg {
+    int w, qsub;
+};
+
+PrefillCfg prefill_cfg() {
+    static PrefillCfg cfg = [] {
+        PrefillCfg c{8, 1};
+        if (const char *e = std::getenv("TECOOPS_FA_PREFILL")) {
+            int w = 0, q = 0;
+            if (std::sscanf(e, "%d,%d", &w, &q) == 2 &&
+                ((w == 4 && q == 1) || (w == 8 && q == 1) || (w == 4 && q == 2)))
+                c = PrefillCfg{w, q};
+        }
+        return c;
+    }();
+    return cfg;
+}
+
+template <typename T, int D, int W, int HW, int QSUB, bool POW2>
+tecoopsStatus_t launch_prefill(const FaParams &p, int max_q, hipStream_t s) {
+    constexpr int QT = 32 * QSUB * (W / HW);
+    auto *kern = &fa_prefill_kernel<T, D, W, HW, QSUB, POW2>;
+    const size_t lds = prefill_lds_bytes<D>();
+    if (!reserve_lds(reinterpret_cast<const void *>(kern), lds)) return TECOOPS_STATUS_INTERNAL_ERROR;
+    dim3 grid(p.batch * p.Hkv * (p.G / HW), (max_q + QT - 1) / QT);
+    hipLaunchKernelGGL(kern, grid, dim3(W * 64), lds, s, p);
+    TECO_CHECK_LAUNCH("flash_attention prefill");
+    return TECOOPS_STATUS_SUCCESS;
+}
+
+template <typename T, int D, int W, int QSUB, bool POW2>
+tecoopsStatus_t prefill_hw(const FaParams &p, int max_q, hipStream_t s) {
+    const int G = p.G;
+    if (G % 4 == 0) return launch_prefill<T, D, W, 4, QSUB, POW2>(p, max_q, s);
+    if (G % 2 == 0) return launch_prefill<T, D, W, 2, QSUB, POW2>(p, max_q, s);
+    return launch_prefill<T, D, W, 1, QSUB, POW2>(p, max_q, s);
+}
+
 template <typename T, int D>
 tecoopsStatus_t run(tecoopsHandle_t handle, FaParams &p, const Plan &pl, int max_q) {
     hipStream_t s = handle->stream;
+    const bool pow2 = p.lbs >= 0;
     if (pl.decode) {
         const size_t lds = decode_lds_bytes<D>();
-        static bool attr_set = false;  // per template instance
-        if (!attr_set) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void *>(&fa_decode_kernel<T, D>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(lds)) != hipSuccess) {
-                (void)hipGetLastError();
-                TECO_ERROR("flash_attention: cannot reserve %zu bytes of LDS", lds);
-                return TECOOPS_STATUS_INTERNAL_ERROR;
-            }
-            attr_set = true;
-        }
+        auto *kern = pow2 ? &fa_decode_kernel<T, D, true> : &fa_decode_kernel<T, D, false>;
+        if (!reserve_lds(reinterpret_cast<const void *>(kern), lds)) return TECOOPS_STATUS_INTERNAL_ERROR;
         dim3 grid(p.batch * p.Hkv, pl.max_splits);
-        hipLaunchKernelGGL((fa_decode_kernel<T, D>), grid, dim3(256), lds, s, p);
+        hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, p);
         TECO_CHECK_LAUNCH("flash_attention decode");
         hipLaunchKernelGGL((fa_decode_combine_kernel<T, D>), dim3(p.batch * p.Hkv), dim3(256), 0,
                            s, p);
         TECO_CHECK_LAUNCH("flash_attention combine");
         return TECOOPS_STATUS_SUCCESS;
     }
-    const int G = p.G;
-    const int HW = (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1);
-    constexpr int QSUB = 1;
-    const int QT = 32 * QSUB * (4 / HW);
-    dim3 grid(p.batch * p.Hkv * (G / HW), (max_q + QT - 1) / QT);
-    switch (HW) {
-        case 4: hipLaunchKernelGGL((fa_prefill_kernel<T, D, 4, QSUB>), grid, dim3(256), 0, s, p); break;
-        case 2: hipLaunchKernelGGL((fa_prefill_kernel<T, D, 2, QSUB>), grid, dim3(256), 0, s, p); break;
-        default: hipLaunchKernelGGL((fa_prefill_kernel<T, D, 1, QSUB>), grid, dim3(256), 0, s, p); break;
+    if (!pow2 || D != 128) {
+        return pow2 ? prefill_hw<T, D, 4, 1, true>(p, max_q, s)
+                    : prefill_hw<T, D, 4, 1, false>(p, max_q, s);
     }
-    TECO_CHECK_LAUNCH("flash_attention prefill");
-    return TECOOPS_STATUS_SUCCESS;
+    const PrefillCfg c = prefill_cfg();
+    if (c.w == 8) return prefill_hw<T, D, 8, 1, true>(p, max_q, s);
+    if (c.qsub == 2) return prefill_hw<T, D, 4, 2, true>(p, max_q, s);
+    return prefill_hw<T, D, 4, 1, true>(p, max_q, s);
 }
 
 bool is_packed_rowmajor(const tecoopsTensorStruct *d) {
@@ -679,7 +804,9 @@ extern "C" tecoopsStatus_t tecoopsFlashAttentionEx(
     p.Hkv = Hkv;
     p.G = H / Hkv;
     p.bs = bs;
+    p.lbs = (bs & (bs - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(bs)) : -1;
     p.num_blocks = num_blocks;
+    p.page_stride = static_cast<long long>(Hkv) * bs * D;
     const float scale = softmax_scale > 0.0f ? softmax_scale : 1.0f / std::sqrt(static_cast<float>(D));
     p.scale_log2 = scale * 1.4426950408889634f;
     p.causal = causal != 0;
