@@ -12,11 +12,13 @@ inputs already resident in HBM (synthetic seeded data):
   gemv_i8_b{1,8}  W int8 [14336, 4096] + fp16 scales
   fa_prefill      bf16 q [4, 32, 4096, 128], k/v [4, 8, 4096, 128], causal
   fa_decode       bf16 B=64, 1 token, paged block 16, kv_len ~ U{512..8192}
-Between two ops a 512 MiB buffer is rewritten (outside the per-op timing) so
-no op reads its inputs from the 256 MiB MALL / L2 left warm by the previous
-step.  Per-op kernel time: torch.cuda events on the stream the ops are
-enqueued on (tecoops binds the current torch stream), averaged over the K
-timed steps.
+Each op cycles through enough copies of its inputs/outputs (>= 1 GiB in
+total, 4x the 256 MiB MALL) that no launch finds its data in L2 / MALL; in
+this steady state an op's HBM traffic per launch equals its algorithmic bytes
+(its own dirty outputs are written back during later launches).  Per-op kernel
+time: K back-to-back launches of the op between one pair of torch.cuda events
+on the stream the ops are enqueued on (tecoops binds the current torch
+stream), divided by K.
 
 Prints ONE JSON line.  `value` is flash-attention prefill TFLOP/s (causal
 FLOP count / average kernel time), the throughput figure of BASELINE.json's
@@ -55,7 +57,6 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-flush", action="store_true")
     ap.add_argument("--ops", default="")
     ap.add_argument("--cpu-threads", type=int, default=0)
     return ap.parse_args()
@@ -78,8 +79,18 @@ def seeded_bits(rng, shape, kind="normal", scale=1.0, lo=0.0, hi=1.0, dtype="f16
     return t.to(torch.float16 if dtype == "f16" else torch.bfloat16)
 
 
+ROTATE_BYTES = 1 << 30   # rotating working set per op: 4x the 256 MiB MALL
+
+
+def copies_for(ws_bytes, limit=16):
+    return max(1, min(limit, -(-ROTATE_BYTES // max(ws_bytes, 1))))
+
+
 def build_ops():
-    """Allocates every op's inputs on the GPU; returns {name: (launch, work)}."""
+    """Allocates every op's inputs on the GPU.  Returns {name: (launches, work)}
+    where launches is a list of closures, one per rotating copy of the op's
+    inputs and outputs (enough copies that consecutive launches never find
+    their data in L2 / MALL)."""
     import torch
     import tecoops
 
@@ -87,52 +98,66 @@ def build_ops():
     ops = {}
 
     # rms_norm [4096, 4096]
-    x = seeded_bits(rng, (4096, 4096))
+    ws = 2 * 4096 * 4096 * 2
     w = seeded_bits(rng, (4096,), "uniform", lo=0.5, hi=1.5)
-    y = torch.empty_like(x)
-    ops["rms_norm"] = (lambda: tecoops.rms_norm(x, w, None, y, None, 1e-6),
-                       dict(bytes=2 * 4096 * 4096 * 2 + 4096 * 2))
+    fns = []
+    for _ in range(copies_for(ws)):
+        x = seeded_bits(rng, (4096, 4096))
+        y = torch.empty_like(x)
+        fns.append(lambda x=x, y=y: tecoops.rms_norm(x, w, None, y, None, 1e-6))
+    ops["rms_norm"] = (fns, dict(bytes=2 * 4096 * 4096 * 2 + 4096 * 2))
 
-    # reshape_and_cache
+    # reshape_and_cache: 8192 tokens into 1024 blocks x 16 slots
     T, Hkv, D, NB, BS = 8192, 8, 128, 1024, 16
-    key = seeded_bits(rng, (T, Hkv, D))
-    val = seeded_bits(rng, (T, Hkv, D))
+    ws = 4 * T * Hkv * D * 2
     slots = torch.from_numpy(rng.permutation(NB * BS)[:T].astype(np.int64)).cuda()
-    kc = torch.zeros((NB, Hkv, BS, D), dtype=torch.float16, device="cuda")
-    vc = torch.zeros_like(kc)
-    ops["reshape_and_cache"] = (
-        lambda: tecoops.reshape_and_cache(key, val, slots, kc, vc),
-        dict(bytes=4 * T * Hkv * D * 2 + T * 8))
+    fns = []
+    for _ in range(copies_for(ws)):
+        key = seeded_bits(rng, (T, Hkv, D))
+        val = seeded_bits(rng, (T, Hkv, D))
+        kc = torch.zeros((NB, Hkv, BS, D), dtype=torch.float16, device="cuda")
+        vc = torch.zeros_like(kc)
+        fns.append(lambda key=key, val=val, kc=kc, vc=vc:
+                   tecoops.reshape_and_cache(key, val, slots, kc, vc))
+    ops["reshape_and_cache"] = (fns, dict(bytes=4 * T * Hkv * D * 2 + T * 8))
 
     # causal_conv1d [8, 4096, 2048]
     B, C, L = 8, 4096, 2048
-    cx = seeded_bits(rng, (B, C, L))
+    ws = 2 * B * C * L * 2
     cw = seeded_bits(rng, (C, 4), scale=0.5)
     cb = seeded_bits(rng, (C,))
-    co = torch.empty_like(cx)
-    cst = torch.zeros((B, 3, C), dtype=torch.float16, device="cuda")
-    ops["causal_conv1d"] = (
-        lambda: tecoops.causal_conv1d(cx, cw, cb, co, conv_states=cst),
-        dict(bytes=2 * B * C * L * 2 + C * 4 * 2 + C * 2 + B * 3 * C * 2))
+    fns = []
+    for _ in range(copies_for(ws)):
+        cx = seeded_bits(rng, (B, C, L))
+        co = torch.empty_like(cx)
+        cst = torch.zeros((B, 3, C), dtype=torch.float16, device="cuda")
+        fns.append(lambda cx=cx, co=co, cst=cst: tecoops.causal_conv1d(cx, cw, cb, co,
+                                                                         conv_states=cst))
+    ops["causal_conv1d"] = (fns, dict(bytes=2 * B * C * L * 2 + C * 4 * 2 + C * 2 + B * 3 * C * 2))
 
-    # rotary
-    q = seeded_bits(rng, (8192, 32, 128))
-    k = seeded_bits(rng, (8192, 8, 128))
+    # rotary (in place)
+    ws = 2 * (8192 * 40 * 128) * 2
     pos = torch.from_numpy((np.arange(8192) % 2048).astype(np.int64)).cuda()
-    ops["rotary"] = (lambda: tecoops.rotary_embedding(pos, q, k, 128),
-                     dict(bytes=2 * (q.numel() + k.numel()) * 2 + 8192 * 8))
+    fns = []
+    for _ in range(copies_for(ws)):
+        q = seeded_bits(rng, (8192, 32, 128))
+        k = seeded_bits(rng, (8192, 8, 128))
+        fns.append(lambda q=q, k=k: tecoops.rotary_embedding(pos, q, k, 128))
+    ops["rotary"] = (fns, dict(bytes=2 * (8192 * 40 * 128) * 2 + 8192 * 8))
 
-    # GEMV
+    # GEMV: W fp16 / int8 [14336, 4096]
     N, K = 14336, 4096
-    W = seeded_bits(rng, (N, K), scale=0.02)
-    Wq = torch.from_numpy(rng.integers(-127, 128, (N, K), dtype=np.int8)).cuda()
+    Ws = [seeded_bits(rng, (N, K), scale=0.02) for _ in range(copies_for(N * K * 2))]
+    Wqs = [torch.from_numpy(rng.integers(-127, 128, (N, K), dtype=np.int8)).cuda()
+           for _ in range(copies_for(N * K))]
     sc = seeded_bits(rng, (N,), "uniform", lo=0.001, hi=0.01)
     for b in (1, 8):
         xv = seeded_bits(rng, (b, K))
         yv = torch.empty((b, N), dtype=torch.float16, device="cuda")
-        ops[f"gemv_f16_b{b}"] = ((lambda xv=xv, yv=yv: tecoops.gemv(W, xv, yv)),
+        ops[f"gemv_f16_b{b}"] = ([lambda W=W, xv=xv, yv=yv: tecoops.gemv(W, xv, yv) for W in Ws],
                                  dict(bytes=N * K * 2 + b * K * 2 + b * N * 2))
-        ops[f"gemv_i8_b{b}"] = ((lambda xv=xv, yv=yv: tecoops.gemv_int8(Wq, sc, xv, yv)),
+        ops[f"gemv_i8_b{b}"] = ([lambda Wq=Wq, xv=xv, yv=yv: tecoops.gemv_int8(Wq, sc, xv, yv)
+                                 for Wq in Wqs],
                                 dict(bytes=N * K + N * 2 + b * K * 2 + b * N * 2))
 
     # flash attention prefill: identity block tables over 4 x 256 blocks
@@ -146,8 +171,8 @@ def build_ops():
     sk = torch.full((FA_B,), FA_S, dtype=torch.int32, device="cuda")
     scale = 1.0 / math.sqrt(FA_D)
     ops["fa_prefill"] = (
-        lambda: tecoops.flash_attn_varlen_func(fq, fk, fv, FA_S, cu, FA_S, None, sk, scale, True,
-                                               None, bt, False, fo),
+        [lambda: tecoops.flash_attn_varlen_func(fq, fk, fv, FA_S, cu, FA_S, None, sk, scale, True,
+                                                None, bt, False, fo)],
         dict(flops=FA_PREFILL_FLOP, bytes=(fq.numel() * 2 + fk.numel() * 2) * 2))
 
     # flash attention decode: B=64, seeded lengths U{512..8192}, shuffled blocks
@@ -170,8 +195,8 @@ def build_ops():
     dsk = torch.from_numpy(lens.astype(np.int32)).cuda()
     sum_l = int(lens.sum())
     ops["fa_decode"] = (
-        lambda: tecoops.flash_attn_varlen_func(dq, dk, dv, 1, dcu, int(lens.max()), None, dsk,
-                                               scale, True, None, dbt, False, do),
+        [lambda: tecoops.flash_attn_varlen_func(dq, dk, dv, 1, dcu, int(lens.max()), None, dsk,
+                                                scale, True, None, dbt, False, do)],
         dict(bytes=4096 * sum_l + 2 * dq.numel() * 2 + DB * 512 * 4,
              flops=4 * FA_H * FA_D * sum_l, sum_kv=sum_l))
     return ops
@@ -230,37 +255,30 @@ def main():
     if args.ops:
         keep = set(args.ops.split(","))
         ops = {k: v for k, v in ops.items() if k in keep}
-    flush = None if args.no_flush else torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
-
-    def run_step(events=None):
-        for name, (fn, _) in ops.items():
-            if flush is not None:
-                flush.zero_()
-            if events is not None:
-                events[name][0].record()
-            fn()
-            if events is not None:
-                events[name][1].record()
-
-    for _ in range(args.warmup):
-        run_step()
+    # Warm-up, then the timed region: K steps, a step being one launch of
+    # every op.  Launches of one op run back to back (rotating over its input
+    # copies) between one pair of events on the stream they are enqueued on,
+    # so the average per launch excludes host overhead.
+    for fns, _ in ops.values():
+        for i in range(args.warmup):
+            fns[i % len(fns)]()
     torch.cuda.synchronize()
-    ev = {n: [] for n in ops}
+    ev = {}
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        e = {n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for n in ops}
-        run_step(e)
-        for n in ops:
-            ev[n].append(e[n])
+    for n, (fns, _) in ops.items():
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(args.steps):
+            fns[i % len(fns)]()
+        b.record()
+        ev[n] = (a, b)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
     report = {}
-    for n, (_, work) in ops.items():
-        ms = [a.elapsed_time(b) for a, b in ev[n]]
-        us = 1e3 * float(np.mean(ms))
-        r = {"us": round(us, 3), "us_median": round(1e3 * float(np.median(ms)), 3)}
+    for n, (fns, work) in ops.items():
+        us = 1e3 * ev[n][0].elapsed_time(ev[n][1]) / args.steps
+        r = {"us": round(us, 3), "rotating_copies": len(fns)}
         if "flops" in work and n == "fa_prefill":
             tf = work["flops"] / (us * 1e-6) / 1e12
             r.update(tflops=round(tf, 2), frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4), bound="mfma")
@@ -305,7 +323,8 @@ def main():
                         "S4096 D128 causal)",
             "fa_prefill": "q [4,32,4096,128], kv [4,8,4096,128], causal, scale 1/sqrt(128)",
             "fa_decode": "B=64, H=32, Hkv=8, D=128, block 16, kv_len seeded U{512..8192}",
-            "l2_flush_between_ops": flush is not None,
+            "rotating_input_copies": "each op cycles through copies of its inputs totalling "
+                                     ">= 1 GiB (4x the MALL) so no launch reads cached data",
         },
         "ops": report,
         "roofline": roof,

@@ -47,26 +47,16 @@ struct ConvArgs {
     int nchunks;
 };
 
+// SiLU v / (1 + e^-v) with the hardware exp2 and reciprocal (about 1 ulp
+// each); saturates correctly to 0 / v for large |v|.
 __device__ __forceinline__ float act(float v, int silu) {
-    return silu ? v / (1.0f + expf(-v)) : v;
+    if (!silu) return v;
+    const float e = __builtin_amdgcn_exp2f(-v * 1.4426950408889634f);
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 template <int W, bool SEQ_CONTIG, int CH>
-__global__ void __launch_bounds__(256) conv1d_kernel(ConvArgs a) {
-    const long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
-    int b, d, c;
-    if (SEQ_CONTIG) {  // chunk fastest
-        c = static_cast<int>(idx % a.nchunks);
-        const long long r = idx / a.nchunks;
-        d = static_cast<int>(r % a.dim);
-        b = static_cast<int>(r / a.dim);
-    } else {  // channel fastest
-        d = static_cast<int>(idx % a.dim);
-        const long long r = idx / a.dim;
-        c = static_cast<int>(r % a.nchunks);
-        b = static_cast<int>(r / a.nchunks);
-    }
-    if (b >= a.batch) return;
+__device__ __forceinline__ void conv1d_body(const ConvArgs &a, int b, int d, int c) {
     long long len, xoff, ooff;
     if (a.qsl != nullptr) {
         const long long s = a.qsl[b];
@@ -157,21 +147,143 @@ __global__ void __launch_bounds__(256) conv1d_kernel(ConvArgs a) {
     }
 }
 
+// Token-contiguous rows ([batch, dim, seqlen] and the reference's
+// [dim, tokens]): lane c of a (sequence, channel) row owns tokens
+// [8c, 8c + 8) and reads one 16-byte vector; the W-1 inputs before its chunk
+// are the last values of lane c-1's vector, taken with a lane shuffle (only the
+// first lane of each wave loads them).  grid = (chunk blocks, channels, batch).
+template <int W>
+__global__ void __launch_bounds__(256) conv1d_contig_kernel(ConvArgs a) {
+    constexpr int CH = 8;
+    const int b = blockIdx.z;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    long long len, xoff, ooff;
+    if (a.qsl != nullptr) {
+        const long long s = a.qsl[b];
+        len = a.qsl[b + 1] - s;
+        xoff = s * a.xs;
+        ooff = s * a.os;
+    } else {
+        len = a.seq_len;
+        xoff = b * a.xb;
+        ooff = b * a.ob;
+    }
+    const int cidx = a.cidx ? a.cidx[b] : b;
+    if (cidx == a.pad_slot_id) return;  // uniform over the workgroup
+    if (static_cast<long long>(blockIdx.x) * blockDim.x * CH >= len) return;
+    const bool use_state =
+        a.state != nullptr && (a.api_mode == 1 || (a.hinit != nullptr && a.hinit[b] != 0));
+    for (int d = blockIdx.y; d < a.dim; d += gridDim.y) {
+        const uint16_t *xr = a.x + xoff + d * a.xd;
+        uint16_t *outr = a.out + ooff + d * a.od;
+        uint16_t *st = a.state ? a.state + static_cast<long long>(cidx) * a.state_stride + d : nullptr;
+        const long long t0 = static_cast<long long>(c) * CH;
+        const bool full = t0 + CH <= len;
+        const bool vec = full && tecoops::aligned(xr + t0, 16);
+        float v[CH];
+        uint32_t dw[4];
+        if (vec) {
+            const uint4 q = *reinterpret_cast<const uint4 *>(xr + t0);
+            dw[0] = q.x; dw[1] = q.y; dw[2] = q.z; dw[3] = q.w;
+        } else {
+            uint16_t e[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) e[j] = (t0 + j < len) ? xr[t0 + j] : 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dw[j] = e[2 * j] | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = lo<f16>(dw[j]);
+            v[2 * j + 1] = hi<f16>(dw[j]);
+        }
+        // last 4 values of the previous lane's chunk (all lanes take part)
+        const uint32_t p2 = __shfl_up(dw[2], 1, 64);
+        const uint32_t p3 = __shfl_up(dw[3], 1, 64);
+        float prev[3] = {hi<f16>(p2), lo<f16>(p3), hi<f16>(p3)};  // tokens t0-3, t0-2, t0-1
+        uint16_t prefix[3] = {0, 0, 0};
+        if (c == 0) {
+#pragma unroll
+            for (int k = 0; k < W - 1; ++k)
+                prefix[k] = use_state ? st[static_cast<long long>(k) * a.dim] : 0;
+#pragma unroll
+            for (int k = 0; k < W - 1; ++k) prev[3 - (W - 1) + k] = h2f(prefix[k]);
+        } else if (lane == 0 && t0 < len) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) prev[k] = h2f(xr[t0 - 3 + k]);
+        }
+        if (t0 < len) {
+            float wv[W];
+#pragma unroll
+            for (int k = 0; k < W; ++k) wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
+            const float bv = a.bias ? h2f(a.bias[d]) : 0.0f;
+            float win[W - 1 + CH];
+#pragma unroll
+            for (int k = 0; k < W - 1; ++k) win[k] = prev[3 - (W - 1) + k];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) win[W - 1 + j] = v[j];
+            float o[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < W; ++k) acc += win[j + k] * wv[k];
+                o[j] = act(acc + bv, a.silu);
+            }
+            if (vec && tecoops::aligned(outr + t0, 16)) {
+                uint4 q;
+                q.x = pack<f16>(o[0], o[1]);
+                q.y = pack<f16>(o[2], o[3]);
+                q.z = pack<f16>(o[4], o[5]);
+                q.w = pack<f16>(o[6], o[7]);
+                *reinterpret_cast<uint4 *>(outr + t0) = q;
+            } else {
+#pragma unroll
+                for (int j = 0; j < CH; ++j)
+                    if (t0 + j < len) outr[t0 + j] = f2h(o[j]);
+            }
+            if (c == 0 && st != nullptr) {
+                uint16_t ns[W - 1];
+#pragma unroll
+                for (int k = 0; k < W - 1; ++k) {
+                    const long long src = len - (W - 1) + k;
+                    ns[k] = src >= 0 ? xr[src] : prefix[W - 1 + src];
+                }
+#pragma unroll
+                for (int k = 0; k < W - 1; ++k) st[static_cast<long long>(k) * a.dim] = ns[k];
+            }
+        }
+    }
+}
+
+template <int W, bool SEQ_CONTIG, int CH>
+__global__ void __launch_bounds__(256) conv1d_kernel(ConvArgs a) {
+    // SEQ_CONTIG: grid (chunk blocks, channels, batch), chunk fastest;
+    // otherwise: grid (channel blocks, chunks, batch), channel fastest.
+    const int b = blockIdx.z;
+    const int lin = blockIdx.x * blockDim.x + threadIdx.x;
+    for (int y = blockIdx.y; y < (SEQ_CONTIG ? a.dim : a.nchunks); y += gridDim.y) {
+        const int c = SEQ_CONTIG ? lin : y;
+        const int d = SEQ_CONTIG ? y : lin;
+        if ((SEQ_CONTIG ? c >= a.nchunks : d >= a.dim)) return;
+        conv1d_body<W, SEQ_CONTIG, CH>(a, b, d, c);
+    }
+}
+
 template <int W>
 void launch(const ConvArgs &a0, bool seq_contig, long long max_len, hipStream_t s) {
     ConvArgs a = a0;
     if (seq_contig) {
         constexpr int CH = 8;
         a.nchunks = static_cast<int>((max_len + CH - 1) / CH);
-        const long long total = static_cast<long long>(a.batch) * a.dim * a.nchunks;
-        hipLaunchKernelGGL((conv1d_kernel<W, true, CH>), dim3(tecoops::ceil_div(total, 256)),
-                           dim3(256), 0, s, a);
+        dim3 grid(tecoops::ceil_div(a.nchunks, 256), a.dim < 65535 ? a.dim : 65535, a.batch);
+        hipLaunchKernelGGL((conv1d_contig_kernel<W>), grid, dim3(256), 0, s, a);
     } else {
         constexpr int CH = 16;
         a.nchunks = static_cast<int>((max_len + CH - 1) / CH);
-        const long long total = static_cast<long long>(a.batch) * a.dim * a.nchunks;
-        hipLaunchKernelGGL((conv1d_kernel<W, false, CH>), dim3(tecoops::ceil_div(total, 256)),
-                           dim3(256), 0, s, a);
+        dim3 grid(tecoops::ceil_div(a.dim, 256), a.nchunks < 65535 ? a.nchunks : 65535, a.batch);
+        hipLaunchKernelGGL((conv1d_kernel<W, false, CH>), grid, dim3(256), 0, s, a);
     }
 }
 
@@ -189,6 +301,7 @@ extern "C" tecoopsStatus_t tecoopsCausalConv1dEx(
     if (handle == nullptr) return TECOOPS_STATUS_NOT_INITIALIZED;
     if (x == nullptr || weight == nullptr || out == nullptr) return TECOOPS_STATUS_BAD_PARAM;
     if (batch <= 0 || seqLen <= 0 || dim <= 0 || width <= 0) return TECOOPS_STATUS_BAD_PARAM;
+    if (batch > 65535) return TECOOPS_STATUS_NOT_SUPPORTED;  // grid z limit
     if (width < 2 || width > 4) {
         TECO_ERROR("causal_conv1d: width %d not supported (2..4)", width);
         return TECOOPS_STATUS_NOT_SUPPORTED;

@@ -5,7 +5,10 @@
 //   fp16 / bf16:  y[b, n] = T( sum_k W[n, k] * x[b, k] )            fp32 acc
 //   int8:         y[b, n] = fp16( s[n] * sum_k float(Wq[n, k]) * x[b, k] )
 //
-// gfx950 design: a workgroup of 4 waves owns 4*R consecutive output rows and
+// gfx950 design: batches of 3+ (fp16 / bf16) or 2+ (int8) rows of x with K a
+// multiple of 32 / 64 run on the matrix cores, see "MFMA path" below, in
+// slices of 16 columns.  Batch 1-2 (and other shapes) take the VALU path,
+// which streams W fastest when there is little math per byte: a workgroup of 4 waves owns 4*R consecutive output rows and
 // first stages x ([B, K], at most 64 KiB) in LDS.  Each wave streams R rows of
 // W with 16-byte loads, lane-interleaved along K so that every load
 // instruction reads a contiguous 1 KiB run of a row, and keeps R x B fp32
@@ -165,6 +168,151 @@ gemv_i8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
     }
 }
 
+// ------------------------------------------------------------------ MFMA path
+//
+// Y^T = W X^T on v_mfma_f32_16x16x32_{f16,bf16}: A = 16 rows of W x 32 k,
+// B = X^T (32 k x 16 batch columns, columns >= B are zero).  Lane l supplies
+// A[row l%16][k 8*(l/16) .. +7] (one 16-byte load of W) and
+// B[k 8*(l/16) .. +7][column l%16] (one 16-byte load of x, L2-resident); it
+// receives C[row 4*(l/16) + v][column l%16], v < 4.  A workgroup owns RT*16
+// rows; its 4 waves take interleaved 32-k steps (split-K) and add their
+// partial C tiles through LDS.  For int8 weights a lane loads 16 weights
+// (16 bytes), widens them exactly to fp16 and feeds two MFMAs whose k order
+// is permuted consistently on A and B (k is a summation index).
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Mma16;
+template <> struct Mma16<f16> {
+    static __device__ __forceinline__ f32x4_t run(u32x4_t a, u32x4_t b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    }
+};
+template <> struct Mma16<bf16> {
+    static __device__ __forceinline__ f32x4_t run(u32x4_t a, u32x4_t b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    }
+};
+
+__device__ __forceinline__ u32x4_t ld16(const uint16_t *p) {
+    return *reinterpret_cast<const u32x4_t *>(p);
+}
+__device__ __forceinline__ u32x4_t ld16_stream(const void *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+}
+
+// Adds the 4 waves' partial tiles and writes y (scaled by s[n] when given).
+template <typename T, int RT>
+__device__ __forceinline__ void gemv_mfma_epilogue(f32x4_t (&c)[RT], float *red, int n0, int N,
+                                                   int B, uint16_t *y, const uint16_t *scales) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        *reinterpret_cast<f32x4_t *>(red + ((rt * 4 + wave) * 64 + lane) * 4) = c[rt];
+    __syncthreads();
+    // wave w finishes row tile w (RT <= 4)
+    if (wave < RT) {
+        f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+            sum += *reinterpret_cast<const f32x4_t *>(red + ((wave * 4 + w) * 64 + lane) * 4);
+        const int col = lane & 15;
+        if (col < B) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int n = n0 + wave * 16 + 4 * (lane >> 4) + v;
+                if (n < N) {
+                    const float o = scales ? sum[v] * h2f(scales[n]) : sum[v];
+                    y[static_cast<long long>(col) * N + n] = Cvt<T>::from(o);
+                }
+            }
+        }
+    }
+}
+
+template <typename T, int RT>
+__global__ void __launch_bounds__(kThreads)
+gemv16_mfma_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x,
+                   uint16_t *__restrict__ y, int N, int K, int B) {
+    __shared__ __attribute__((aligned(16))) float red[RT * kWaves * 64 * 4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * (16 * RT);
+    const int g = lane >> 4, col = lane & 15;
+    const uint16_t *wr[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        wr[rt] = W + static_cast<long long>(min(n0 + rt * 16 + col, N - 1)) * K + 8 * g;
+    const bool xcol = col < B;
+    const uint16_t *xr = x + static_cast<long long>(min(col, B - 1)) * K + 8 * g;
+    f32x4_t c[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) c[rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const int steps = K / 32;
+#pragma unroll 4
+    for (int st = wave; st < steps; st += kWaves) {
+        const int k0 = st * 32;
+        u32x4_t a[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) a[rt] = ld16_stream(wr[rt] + k0);
+        u32x4_t b = xcol ? ld16(xr + k0) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) c[rt] = Mma16<T>::run(a[rt], b, c[rt]);
+    }
+    gemv_mfma_epilogue<T, RT>(c, red, n0, N, B, y, nullptr);
+}
+
+__device__ __forceinline__ void widen_i8x16(u32x4_t q, u32x4_t &lo8, u32x4_t &hi8) {
+    uint32_t p[8];
+    widen_i8(q.x, p[0], p[1]);
+    widen_i8(q.y, p[2], p[3]);
+    widen_i8(q.z, p[4], p[5]);
+    widen_i8(q.w, p[6], p[7]);
+    lo8 = u32x4_t{p[0], p[1], p[2], p[3]};
+    hi8 = u32x4_t{p[4], p[5], p[6], p[7]};
+}
+
+template <int RT>
+__global__ void __launch_bounds__(kThreads)
+gemv_i8_mfma_kernel(const int8_t *__restrict__ W, const uint16_t *__restrict__ scales,
+                    const uint16_t *__restrict__ x, uint16_t *__restrict__ y, int N, int K,
+                    int B) {
+    __shared__ __attribute__((aligned(16))) float red[RT * kWaves * 64 * 4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * (16 * RT);
+    const int g = lane >> 4, col = lane & 15;
+    const int8_t *wr[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        wr[rt] = W + static_cast<long long>(min(n0 + rt * 16 + col, N - 1)) * K + 16 * g;
+    const bool xcol = col < B;
+    const uint16_t *xr = x + static_cast<long long>(min(col, B - 1)) * K + 16 * g;
+    f32x4_t c[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) c[rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const int steps = K / 64;
+#pragma unroll 4
+    for (int st = wave; st < steps; st += kWaves) {
+        const int k0 = st * 64;
+        u32x4_t q[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) q[rt] = ld16_stream(wr[rt] + k0);
+        const u32x4_t zero = {0u, 0u, 0u, 0u};
+        const u32x4_t b0 = xcol ? ld16(xr + k0) : zero;
+        const u32x4_t b1 = xcol ? ld16(xr + k0 + 8) : zero;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            u32x4_t a0, a1;
+            widen_i8x16(q[rt], a0, a1);
+            c[rt] = Mma16<f16>::run(a0, b0, c[rt]);
+            c[rt] = Mma16<f16>::run(a1, b1, c[rt]);
+        }
+    }
+    gemv_mfma_epilogue<f16, RT>(c, red, n0, N, B, y, scales);
+}
+
 // Fallback for shapes the vector kernels do not take (K not a multiple of 8 /
 // 16, misaligned pointers): one wave per (row, batch), element-wise.
 template <typename T, bool INT8>
@@ -250,6 +398,23 @@ extern "C" tecoopsStatus_t tecoopsGemv(tecoopsHandle_t handle, const void *weigh
     using tecoops::dev::bf16;
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
+    if (batch > 2 && (k % 32) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16)) {
+        constexpr int RT = 1;
+        for (int b0 = 0; b0 < batch; b0 += 16) {
+            const int nb = batch - b0 < 16 ? batch - b0 : 16;
+            const uint16_t *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
+            uint16_t *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
+            const unsigned grid = tecoops::ceil_div(n, 16 * RT);
+            if (dataType == TECOOPS_DATA_HALF)
+                hipLaunchKernelGGL((gemv16_mfma_kernel<f16, RT>), dim3(grid), dim3(kThreads), 0, s,
+                                   static_cast<const uint16_t *>(weight), xb, yb, n, k, nb);
+            else
+                hipLaunchKernelGGL((gemv16_mfma_kernel<bf16, RT>), dim3(grid), dim3(kThreads), 0,
+                                   s, static_cast<const uint16_t *>(weight), xb, yb, n, k, nb);
+            TECO_CHECK_LAUNCH("gemv");
+        }
+        return TECOOPS_STATUS_SUCCESS;
+    }
     const bool vec = (k % 8) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16) &&
                      8 * k * 2 <= kMaxLdsBytes;
     if (vec) {
@@ -286,6 +451,19 @@ extern "C" tecoopsStatus_t tecoopsGemvInt8(tecoopsHandle_t handle, const int8_t 
     if (batch <= 0 || n <= 0 || k <= 0) return TECOOPS_STATUS_BAD_PARAM;
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
+    if (batch > 1 && (k % 64) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16)) {
+        constexpr int RT = 1;
+        for (int b0 = 0; b0 < batch; b0 += 16) {
+            const int nb = batch - b0 < 16 ? batch - b0 : 16;
+            const uint16_t *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
+            uint16_t *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
+            hipLaunchKernelGGL((gemv_i8_mfma_kernel<RT>), dim3(tecoops::ceil_div(n, 16 * RT)),
+                               dim3(kThreads), 0, s, weight, static_cast<const uint16_t *>(scales),
+                               xb, yb, n, k, nb);
+            TECO_CHECK_LAUNCH("gemv_int8");
+        }
+        return TECOOPS_STATUS_SUCCESS;
+    }
     const bool vec = (k % 16) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16) &&
                      8 * k * 2 <= kMaxLdsBytes;
     if (vec) {

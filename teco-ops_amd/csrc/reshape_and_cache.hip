@@ -10,34 +10,47 @@
 // gfx950 design: one lane per 16-byte chunk of a (token, head) row; a wave
 // covers 1 KiB of contiguous key (and value) bytes, so reads are fully
 // coalesced and every destination run is a whole head_size row.  Each lane
-// moves its key and its value chunk, i.e. 32 B in flight per lane.  HBM-bound:
-// algorithmic bytes = 4 * num_tokens * H * D * 2 + 8 * num_tokens.
+// moves one key and one value chunk (the access shape that streams fastest
+// on MI355X: one 16-byte vector per lane over a large grid).
+// HBM-bound: algorithmic bytes = 4 * num_tokens * H * D * 2 + 8 * num_tokens.
 #include "common.h"
 
 namespace {
 
-template <typename V>
+// One lane per 16-byte chunk of one (token, head) row, key and value: the
+// grid is (ceil(per_token / 256), num_tokens) so no index division is needed
+// beyond one by vec_per_row.  Slot arithmetic is 32-bit (slots < 2^31 after
+// the range check), with a shift / mask when block_size is a power of two.
+template <typename V, bool POW2>
 __global__ void __launch_bounds__(256)
 reshape_and_cache_kernel(const V *__restrict__ key, const V *__restrict__ value,
                          const int64_t *__restrict__ slot_mapping, V *__restrict__ key_cache,
-                         V *__restrict__ value_cache, long long total, int heads, int vec_per_row,
-                         int block_size, long long capacity) {
-    const long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
-    if (i >= total) return;
+                         V *__restrict__ value_cache, int heads, int vec_per_row, int block_size,
+                         int lbs, long long capacity) {
     const int per_token = heads * vec_per_row;
-    const long long t = i / per_token;
-    const int rem = static_cast<int>(i - t * per_token);
+    const int rem = blockIdx.x * blockDim.x + threadIdx.x;
+    if (rem >= per_token) return;
+    const int t = blockIdx.y;
+    const long long src = static_cast<long long>(t) * per_token + rem;
     const int64_t slot = slot_mapping[t];
+    const V kv = key[src];
+    const V vv = value[src];
     if (slot < 0 || slot >= capacity) return;
+    const int s32 = static_cast<int>(slot);
+    int blk, off;
+    if (POW2) {
+        blk = s32 >> lbs;
+        off = s32 & (block_size - 1);
+    } else {
+        blk = s32 / block_size;
+        off = s32 - blk * block_size;
+    }
     const int h = rem / vec_per_row;
     const int c = rem - h * vec_per_row;
-    const long long blk = slot / block_size;
-    const long long off = slot - blk * block_size;
-    const long long dst = ((blk * heads + h) * block_size + off) * vec_per_row + c;
-    const V k = key[i];
-    const V v = value[i];
-    key_cache[dst] = k;
-    value_cache[dst] = v;
+    const long long dst =
+        ((static_cast<long long>(blk) * heads + h) * block_size + off) * vec_per_row + c;
+    key_cache[dst] = kv;
+    value_cache[dst] = vv;
 }
 
 template <typename V>
@@ -45,14 +58,24 @@ tecoopsStatus_t launch(tecoopsHandle_t handle, const void *key, const void *valu
                        const int64_t *slot_mapping, void *key_cache, void *value_cache,
                        int num_tokens, int heads, int vec_per_row, int num_blocks,
                        int block_size) {
-    const long long total = static_cast<long long>(num_tokens) * heads * vec_per_row;
+    const long long per_token = static_cast<long long>(heads) * vec_per_row;
     const long long capacity = static_cast<long long>(num_blocks) * block_size;
-    hipLaunchKernelGGL(reshape_and_cache_kernel<V>, dim3(tecoops::ceil_div(total, 256)),
-                       dim3(256), 0, handle->stream, static_cast<const V *>(key),
-                       static_cast<const V *>(value), slot_mapping, static_cast<V *>(key_cache),
-                       static_cast<V *>(value_cache), total, heads, vec_per_row, block_size,
-                       capacity);
-    TECO_CHECK_LAUNCH("reshape_and_cache");
+    if (capacity >= (1ll << 31) || per_token >= (1ll << 31)) {
+        TECO_ERROR("reshape_and_cache: sizes beyond the supported index range");
+        return TECOOPS_STATUS_NOT_SUPPORTED;
+    }
+    const int lbs = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
+    auto *kern = lbs >= 0 ? &reshape_and_cache_kernel<V, true> : &reshape_and_cache_kernel<V, false>;
+    // grid.y is limited to 65535: longer token ranges run in slices
+    for (int t0 = 0; t0 < num_tokens; t0 += 65535) {
+        const int nt = num_tokens - t0 < 65535 ? num_tokens - t0 : 65535;
+        hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(per_token, 256), nt), dim3(256), 0,
+                           handle->stream, static_cast<const V *>(key) + t0 * per_token,
+                           static_cast<const V *>(value) + t0 * per_token, slot_mapping + t0,
+                           static_cast<V *>(key_cache), static_cast<V *>(value_cache), heads,
+                           vec_per_row, block_size, lbs, capacity);
+        TECO_CHECK_LAUNCH("reshape_and_cache");
+    }
     return TECOOPS_STATUS_SUCCESS;
 }
 

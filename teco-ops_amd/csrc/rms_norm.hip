@@ -7,12 +7,13 @@
 //         unrounded v; y = T(float(T(v)) * rstd * w)
 // fp32 accumulation throughout.
 //
-// gfx950 design: one workgroup per row.  Each lane keeps its VPT 16-byte
-// chunks of the row in registers between the reduction and the output pass,
-// so x (and r) are read from HBM exactly once; the sum of squares is reduced
-// across the wave with xor-shuffles and across waves through LDS.  For rows
-// that do not fit the register path (D % 8 != 0 or D > 8*256*8) a two-pass
-// loop reads the row twice (the second read hits L2).  HBM-bound:
+// gfx950 design: rows up to 8192 elements (16-byte aligned, D % 8 == 0) run
+// one wave per row: each lane keeps its chunks of the row in registers
+// between the reduction and the output pass, so x (and r) are read from HBM
+// exactly once and the sum of squares is a wave-wide xor-shuffle reduction
+// (no LDS, no barrier).  Rows up to 16384 use a 256-lane workgroup per row
+// with an LDS reduction across its 4 waves.  Other rows (D % 8 != 0,
+// misaligned, wider) take a two-pass element loop (second read hits L2).  HBM-bound:
 // algorithmic bytes = 2*N*D*2 + 2*D (+ 2*N*D*2 for the add variant).
 #include "common.h"
 #include "device.h"
@@ -94,6 +95,72 @@ rms_norm_vec(const uint4 *__restrict__ x, const uint4 *__restrict__ w, const uin
     }
 }
 
+// One wave per row: each lane holds VPT 16-byte chunks of its row in
+// registers, so the row is read once and the sum of squares needs only a wave
+// reduction (no LDS, no barrier).  4 independent rows per workgroup.
+template <typename T, int VPT, bool ADD>
+__global__ void __launch_bounds__(256)
+rms_norm_wave(const uint4 *__restrict__ x, const uint4 *__restrict__ w, const uint4 *__restrict__ r,
+              uint4 *__restrict__ y, uint4 *__restrict__ r_out, int rows, int vec_per_row,
+              int hidden, float eps) {
+    const int lane = threadIdx.x & 63;
+    const long long row = static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint4 *xr = x + row * vec_per_row;
+    uint4 v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int c = lane + 64 * j;
+        if (c < vec_per_row) v[j] = xr[c];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int c = lane + 64 * j;
+        if (c < vec_per_row) {
+            uint32_t *pa = reinterpret_cast<uint32_t *>(&v[j]);
+            if (ADD) {
+                const uint4 b = r[row * vec_per_row + c];
+                const uint32_t *pb = reinterpret_cast<const uint32_t *>(&b);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float s0 = lo<T>(pa[q]) + lo<T>(pb[q]);
+                    const float s1 = hi<T>(pa[q]) + hi<T>(pb[q]);
+                    ss += s0 * s0;
+                    ss += s1 * s1;
+                    pa[q] = pack<T>(s0, s1);
+                }
+                r_out[row * vec_per_row + c] = v[j];
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float s0 = lo<T>(pa[q]), s1 = hi<T>(pa[q]);
+                    ss += s0 * s0;
+                    ss += s1 * s1;
+                }
+            }
+        }
+    }
+    const float total = wave_sum(ss);
+    const float rstd = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int c = lane + 64 * j;
+        if (c < vec_per_row) {
+            const uint4 wv = w[c];
+            const uint32_t *pa = reinterpret_cast<const uint32_t *>(&v[j]);
+            const uint32_t *pw = reinterpret_cast<const uint32_t *>(&wv);
+            uint4 o;
+            uint32_t *po = reinterpret_cast<uint32_t *>(&o);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                po[q] = pack<T>(lo<T>(pa[q]) * rstd * lo<T>(pw[q]),
+                                hi<T>(pa[q]) * rstd * hi<T>(pw[q]));
+            y[row * vec_per_row + c] = o;
+        }
+    }
+}
+
 // Generic path: any hidden size, element-wise, two passes over the row.
 template <typename T, bool ADD>
 __global__ void __launch_bounds__(kThreads)
@@ -122,6 +189,15 @@ rms_norm_scalar(const uint16_t *__restrict__ x, const uint16_t *__restrict__ w,
 }
 
 template <typename T, int VPT, bool ADD>
+void launch_wave(const void *x, const void *w, const void *r, void *y, void *ro, int rows,
+                 int hidden, float eps, hipStream_t s) {
+    hipLaunchKernelGGL((rms_norm_wave<T, VPT, ADD>), dim3(tecoops::ceil_div(rows, 4)), dim3(256),
+                       0, s, static_cast<const uint4 *>(x), static_cast<const uint4 *>(w),
+                       static_cast<const uint4 *>(r), static_cast<uint4 *>(y),
+                       static_cast<uint4 *>(ro), rows, hidden / 8, hidden, eps);
+}
+
+template <typename T, int VPT, bool ADD>
 void launch_vec(int threads, const void *x, const void *w, const void *r, void *y, void *ro,
                 int rows, int hidden, float eps, hipStream_t s) {
     hipLaunchKernelGGL((rms_norm_vec<T, VPT, ADD>), dim3(rows), dim3(threads), 0, s,
@@ -138,7 +214,15 @@ tecoopsStatus_t dispatch(tecoopsHandle_t handle, const void *x, const void *w, c
     for (const void *p : {x, w, r, static_cast<const void *>(y), static_cast<const void *>(ro)})
         if (p != nullptr) vec = vec && tecoops::aligned(p, 16);
     const int nvec = hidden / 8;
-    if (vec && nvec <= kThreads * 8) {
+    if (vec && nvec <= 64 * 16) {
+        // up to 16 chunks (8 KiB of fp16 row at 4096 hidden = 8 chunks) per lane
+        const int vpt = (nvec + 63) / 64;
+        if (vpt <= 1) launch_wave<T, 1, ADD>(x, w, r, y, ro, rows, hidden, eps, s);
+        else if (vpt <= 2) launch_wave<T, 2, ADD>(x, w, r, y, ro, rows, hidden, eps, s);
+        else if (vpt <= 4) launch_wave<T, 4, ADD>(x, w, r, y, ro, rows, hidden, eps, s);
+        else if (vpt <= 8) launch_wave<T, 8, ADD>(x, w, r, y, ro, rows, hidden, eps, s);
+        else launch_wave<T, 16, ADD>(x, w, r, y, ro, rows, hidden, eps, s);
+    } else if (vec && nvec <= kThreads * 8) {
         // Narrow rows use one wave; wide rows 256 lanes with up to 8 chunks each.
         const int threads = nvec <= 64 ? 64 : (nvec <= 128 ? 128 : kThreads);
         const int vpt = (nvec + threads - 1) / threads;

@@ -31,22 +31,28 @@ __all__ = [
     "rotary_embedding", "gemv", "gemv_int8", "causal_conv1d", "memset",
 ]
 
-_handles = {}
+_handles = {}   # device index -> [handle, bound stream]
 _lock = threading.Lock()
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def _handle(device):
-    """Per-device handle bound to the device's current torch stream."""
+    """Per-device handle bound to the device's current torch stream (rebound
+    only when the current stream changes)."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    with _lock:
-        h = _handles.get(idx)
-        if h is None:
-            h = ctypes.c_void_p()
-            _lib.call("tecoopsCreate", ctypes.byref(h))
-            _handles[idx] = h
-    stream = torch.cuda.current_stream(idx).cuda_stream
-    _lib.call("tecoopsSetStream", h, ctypes.c_void_p(stream))
-    return h
+    entry = _handles.get(idx)
+    if entry is None:
+        with _lock:
+            entry = _handles.get(idx)
+            if entry is None:
+                h = ctypes.c_void_p()
+                _lib.call("tecoopsCreate", ctypes.byref(h))
+                entry = _handles[idx] = [h, None]
+    stream = _raw_stream(idx) if _raw_stream else torch.cuda.current_stream(idx).cuda_stream
+    if stream != entry[1]:
+        _lib.call("tecoopsSetStream", entry[0], ctypes.c_void_p(stream))
+        entry[1] = stream
+    return entry[0]
 
 
 def _dtype_code(t):

@@ -246,7 +246,7 @@ def test_causal_conv1d_baseline_config():
 
 # -------------------------------------------------------------------------- GEMV
 
-@pytest.mark.parametrize("B", [1, 8, 3, 11])
+@pytest.mark.parametrize("B", [1, 8, 3, 11, 20])
 def test_gemv_fp16(B):
     r = rng(300 + B)
     N, K = (14336, 4096) if B in (1, 8) else (1000, 512)
@@ -259,7 +259,7 @@ def test_gemv_fp16(B):
     assert_close(as_f32(y), ref, what=f"gemv B={B}")
 
 
-@pytest.mark.parametrize("B", [1, 8, 5])
+@pytest.mark.parametrize("B", [1, 8, 5, 17])
 def test_gemv_int8(B):
     r = rng(400 + B)
     N, K = (14336, 4096) if B in (1, 8) else (777, 1024)
