@@ -86,7 +86,7 @@ def copies_for(ws_bytes, limit=16):
     return max(1, min(limit, -(-ROTATE_BYTES // max(ws_bytes, 1))))
 
 
-def build_ops():
+def build_ops(names=None):
     """Allocates every op's inputs on the GPU.  Returns {name: (launches, work)}
     where launches is a list of closures, one per rotating copy of the op's
     inputs and outputs (enough copies that consecutive launches never find
@@ -97,108 +97,119 @@ def build_ops():
     rng = np.random.default_rng(1000)
     ops = {}
 
-    # rms_norm [4096, 4096]
-    ws = 2 * 4096 * 4096 * 2
-    w = seeded_bits(rng, (4096,), "uniform", lo=0.5, hi=1.5)
-    fns = []
-    for _ in range(copies_for(ws)):
-        x = seeded_bits(rng, (4096, 4096))
-        y = torch.empty_like(x)
-        fns.append(lambda x=x, y=y: tecoops.rms_norm(x, w, None, y, None, 1e-6))
-    ops["rms_norm"] = (fns, dict(bytes=2 * 4096 * 4096 * 2 + 4096 * 2))
-
-    # reshape_and_cache: 8192 tokens into 1024 blocks x 16 slots
-    T, Hkv, D, NB, BS = 8192, 8, 128, 1024, 16
-    ws = 4 * T * Hkv * D * 2
-    slots = torch.from_numpy(rng.permutation(NB * BS)[:T].astype(np.int64)).cuda()
-    fns = []
-    for _ in range(copies_for(ws)):
-        key = seeded_bits(rng, (T, Hkv, D))
-        val = seeded_bits(rng, (T, Hkv, D))
-        kc = torch.zeros((NB, Hkv, BS, D), dtype=torch.float16, device="cuda")
-        vc = torch.zeros_like(kc)
-        fns.append(lambda key=key, val=val, kc=kc, vc=vc:
-                   tecoops.reshape_and_cache(key, val, slots, kc, vc))
-    ops["reshape_and_cache"] = (fns, dict(bytes=4 * T * Hkv * D * 2 + T * 8))
-
-    # causal_conv1d [8, 4096, 2048]
-    B, C, L = 8, 4096, 2048
-    ws = 2 * B * C * L * 2
-    cw = seeded_bits(rng, (C, 4), scale=0.5)
-    cb = seeded_bits(rng, (C,))
-    fns = []
-    for _ in range(copies_for(ws)):
-        cx = seeded_bits(rng, (B, C, L))
-        co = torch.empty_like(cx)
-        cst = torch.zeros((B, 3, C), dtype=torch.float16, device="cuda")
-        fns.append(lambda cx=cx, co=co, cst=cst: tecoops.causal_conv1d(cx, cw, cb, co,
-                                                                         conv_states=cst))
-    ops["causal_conv1d"] = (fns, dict(bytes=2 * B * C * L * 2 + C * 4 * 2 + C * 2 + B * 3 * C * 2))
-
-    # rotary (in place)
-    ws = 2 * (8192 * 40 * 128) * 2
-    pos = torch.from_numpy((np.arange(8192) % 2048).astype(np.int64)).cuda()
-    fns = []
-    for _ in range(copies_for(ws)):
-        q = seeded_bits(rng, (8192, 32, 128))
-        k = seeded_bits(rng, (8192, 8, 128))
-        fns.append(lambda q=q, k=k: tecoops.rotary_embedding(pos, q, k, 128))
-    ops["rotary"] = (fns, dict(bytes=2 * (8192 * 40 * 128) * 2 + 8192 * 8))
-
-    # GEMV: W fp16 / int8 [14336, 4096]
-    N, K = 14336, 4096
-    Ws = [seeded_bits(rng, (N, K), scale=0.02) for _ in range(copies_for(N * K * 2))]
-    Wqs = [torch.from_numpy(rng.integers(-127, 128, (N, K), dtype=np.int8)).cuda()
-           for _ in range(copies_for(N * K))]
-    sc = seeded_bits(rng, (N,), "uniform", lo=0.001, hi=0.01)
-    for b in (1, 8):
-        xv = seeded_bits(rng, (b, K))
-        yv = torch.empty((b, N), dtype=torch.float16, device="cuda")
-        ops[f"gemv_f16_b{b}"] = ([lambda W=W, xv=xv, yv=yv: tecoops.gemv(W, xv, yv) for W in Ws],
-                                 dict(bytes=N * K * 2 + b * K * 2 + b * N * 2))
-        ops[f"gemv_i8_b{b}"] = ([lambda Wq=Wq, xv=xv, yv=yv: tecoops.gemv_int8(Wq, sc, xv, yv)
-                                 for Wq in Wqs],
-                                dict(bytes=N * K + N * 2 + b * K * 2 + b * N * 2))
-
-    # flash attention prefill: identity block tables over 4 x 256 blocks
-    nbp = FA_S // 16
-    fq = seeded_bits(rng, (FA_B * FA_S, FA_H, FA_D), dtype="bf16")
-    fk = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
-    fv = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
-    fo = torch.empty_like(fq)
-    bt = torch.arange(FA_B * nbp, dtype=torch.int32, device="cuda").view(FA_B, nbp)
-    cu = torch.arange(0, FA_B + 1, dtype=torch.int32, device="cuda") * FA_S
-    sk = torch.full((FA_B,), FA_S, dtype=torch.int32, device="cuda")
     scale = 1.0 / math.sqrt(FA_D)
-    ops["fa_prefill"] = (
-        [lambda: tecoops.flash_attn_varlen_func(fq, fk, fv, FA_S, cu, FA_S, None, sk, scale, True,
-                                                None, bt, False, fo)],
-        dict(flops=FA_PREFILL_FLOP, bytes=(fq.numel() * 2 + fk.numel() * 2) * 2))
 
-    # flash attention decode: B=64, seeded lengths U{512..8192}, shuffled blocks
-    DB = 64
-    lens = rng.integers(512, 8193, DB)
-    nblk = (lens + 15) // 16
-    tot = int(nblk.sum())
-    perm = rng.permutation(tot)
-    btd = np.zeros((DB, 512), np.int32)
-    i = 0
-    for b in range(DB):
-        btd[b, :nblk[b]] = perm[i:i + nblk[b]]
-        i += nblk[b]
-    dq = seeded_bits(rng, (DB, FA_H, FA_D), dtype="bf16")
-    dk = seeded_bits(rng, (tot, FA_HKV, 16, FA_D), dtype="bf16")
-    dv = seeded_bits(rng, (tot, FA_HKV, 16, FA_D), dtype="bf16")
-    do = torch.empty_like(dq)
-    dbt = torch.from_numpy(btd).cuda()
-    dcu = torch.arange(0, DB + 1, dtype=torch.int32, device="cuda")
-    dsk = torch.from_numpy(lens.astype(np.int32)).cuda()
-    sum_l = int(lens.sum())
-    ops["fa_decode"] = (
-        [lambda: tecoops.flash_attn_varlen_func(dq, dk, dv, 1, dcu, int(lens.max()), None, dsk,
-                                                scale, True, None, dbt, False, do)],
-        dict(bytes=4096 * sum_l + 2 * dq.numel() * 2 + DB * 512 * 4,
-             flops=4 * FA_H * FA_D * sum_l, sum_kv=sum_l))
+    def want(*ns):
+        return names is None or any(n in names for n in ns)
+
+    if want("rms_norm"):
+        # rms_norm [4096, 4096]
+        ws = 2 * 4096 * 4096 * 2
+        w = seeded_bits(rng, (4096,), "uniform", lo=0.5, hi=1.5)
+        fns = []
+        for _ in range(copies_for(ws)):
+            x = seeded_bits(rng, (4096, 4096))
+            y = torch.empty_like(x)
+            fns.append(lambda x=x, y=y: tecoops.rms_norm(x, w, None, y, None, 1e-6))
+        ops["rms_norm"] = (fns, dict(bytes=2 * 4096 * 4096 * 2 + 4096 * 2))
+
+    if want("reshape_and_cache"):
+        # reshape_and_cache: 8192 tokens into 1024 blocks x 16 slots
+        T, Hkv, D, NB, BS = 8192, 8, 128, 1024, 16
+        ws = 4 * T * Hkv * D * 2
+        slots = torch.from_numpy(rng.permutation(NB * BS)[:T].astype(np.int64)).cuda()
+        fns = []
+        for _ in range(copies_for(ws)):
+            key = seeded_bits(rng, (T, Hkv, D))
+            val = seeded_bits(rng, (T, Hkv, D))
+            kc = torch.zeros((NB, Hkv, BS, D), dtype=torch.float16, device="cuda")
+            vc = torch.zeros_like(kc)
+            fns.append(lambda key=key, val=val, kc=kc, vc=vc:
+                       tecoops.reshape_and_cache(key, val, slots, kc, vc))
+        ops["reshape_and_cache"] = (fns, dict(bytes=4 * T * Hkv * D * 2 + T * 8))
+
+    if want("causal_conv1d"):
+        # causal_conv1d [8, 4096, 2048]
+        B, C, L = 8, 4096, 2048
+        ws = 2 * B * C * L * 2
+        cw = seeded_bits(rng, (C, 4), scale=0.5)
+        cb = seeded_bits(rng, (C,))
+        fns = []
+        for _ in range(copies_for(ws)):
+            cx = seeded_bits(rng, (B, C, L))
+            co = torch.empty_like(cx)
+            cst = torch.zeros((B, 3, C), dtype=torch.float16, device="cuda")
+            fns.append(lambda cx=cx, co=co, cst=cst: tecoops.causal_conv1d(cx, cw, cb, co,
+                                                                             conv_states=cst))
+        ops["causal_conv1d"] = (fns, dict(bytes=2 * B * C * L * 2 + C * 4 * 2 + C * 2 + B * 3 * C * 2))
+
+    if want("rotary"):
+        # rotary (in place)
+        ws = 2 * (8192 * 40 * 128) * 2
+        pos = torch.from_numpy((np.arange(8192) % 2048).astype(np.int64)).cuda()
+        fns = []
+        for _ in range(copies_for(ws)):
+            q = seeded_bits(rng, (8192, 32, 128))
+            k = seeded_bits(rng, (8192, 8, 128))
+            fns.append(lambda q=q, k=k: tecoops.rotary_embedding(pos, q, k, 128))
+        ops["rotary"] = (fns, dict(bytes=2 * (8192 * 40 * 128) * 2 + 8192 * 8))
+
+    if want("gemv_f16_b1", "gemv_f16_b8", "gemv_i8_b1", "gemv_i8_b8"):
+        # GEMV: W fp16 / int8 [14336, 4096]
+        N, K = 14336, 4096
+        Ws = [seeded_bits(rng, (N, K), scale=0.02) for _ in range(copies_for(N * K * 2))]
+        Wqs = [torch.from_numpy(rng.integers(-127, 128, (N, K), dtype=np.int8)).cuda()
+               for _ in range(copies_for(N * K))]
+        sc = seeded_bits(rng, (N,), "uniform", lo=0.001, hi=0.01)
+        for b in (1, 8):
+            xv = seeded_bits(rng, (b, K))
+            yv = torch.empty((b, N), dtype=torch.float16, device="cuda")
+            ops[f"gemv_f16_b{b}"] = ([lambda W=W, xv=xv, yv=yv: tecoops.gemv(W, xv, yv) for W in Ws],
+                                     dict(bytes=N * K * 2 + b * K * 2 + b * N * 2))
+            ops[f"gemv_i8_b{b}"] = ([lambda Wq=Wq, xv=xv, yv=yv: tecoops.gemv_int8(Wq, sc, xv, yv)
+                                     for Wq in Wqs],
+                                    dict(bytes=N * K + N * 2 + b * K * 2 + b * N * 2))
+
+    if want("fa_prefill"):
+        # flash attention prefill: identity block tables over 4 x 256 blocks
+        nbp = FA_S // 16
+        fq = seeded_bits(rng, (FA_B * FA_S, FA_H, FA_D), dtype="bf16")
+        fk = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
+        fv = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
+        fo = torch.empty_like(fq)
+        bt = torch.arange(FA_B * nbp, dtype=torch.int32, device="cuda").view(FA_B, nbp)
+        cu = torch.arange(0, FA_B + 1, dtype=torch.int32, device="cuda") * FA_S
+        sk = torch.full((FA_B,), FA_S, dtype=torch.int32, device="cuda")
+        ops["fa_prefill"] = (
+            [lambda: tecoops.flash_attn_varlen_func(fq, fk, fv, FA_S, cu, FA_S, None, sk, scale, True,
+                                                    None, bt, False, fo)],
+            dict(flops=FA_PREFILL_FLOP, bytes=(fq.numel() * 2 + fk.numel() * 2) * 2))
+
+    if want("fa_decode"):
+        # flash attention decode: B=64, seeded lengths U{512..8192}, shuffled blocks
+        DB = 64
+        lens = rng.integers(512, 8193, DB)
+        nblk = (lens + 15) // 16
+        tot = int(nblk.sum())
+        perm = rng.permutation(tot)
+        btd = np.zeros((DB, 512), np.int32)
+        i = 0
+        for b in range(DB):
+            btd[b, :nblk[b]] = perm[i:i + nblk[b]]
+            i += nblk[b]
+        dq = seeded_bits(rng, (DB, FA_H, FA_D), dtype="bf16")
+        dk = seeded_bits(rng, (tot, FA_HKV, 16, FA_D), dtype="bf16")
+        dv = seeded_bits(rng, (tot, FA_HKV, 16, FA_D), dtype="bf16")
+        do = torch.empty_like(dq)
+        dbt = torch.from_numpy(btd).cuda()
+        dcu = torch.arange(0, DB + 1, dtype=torch.int32, device="cuda")
+        dsk = torch.from_numpy(lens.astype(np.int32)).cuda()
+        sum_l = int(lens.sum())
+        ops["fa_decode"] = (
+            [lambda: tecoops.flash_attn_varlen_func(dq, dk, dv, 1, dcu, int(lens.max()), None, dsk,
+                                                    scale, True, None, dbt, False, do)],
+            dict(bytes=4096 * sum_l + 2 * dq.numel() * 2 + DB * 512 * 4,
+                 flops=4 * FA_H * FA_D * sum_l, sum_kv=sum_l))
     return ops
 
 
@@ -251,9 +262,9 @@ def main():
         sys.exit(2)
     import torch
     torch.cuda.set_device(0)
-    ops = build_ops()
-    if args.ops:
-        keep = set(args.ops.split(","))
+    keep = set(args.ops.split(",")) if args.ops else None
+    ops = build_ops(keep)
+    if keep:
         ops = {k: v for k, v in ops.items() if k in keep}
     # Warm-up, then the timed region: K steps, a step being one launch of
     # every op.  Launches of one op run back to back (rotating over its input

@@ -218,6 +218,100 @@ struct TileLoader {
     }
 };
 
+// Loader for D = 128 and a power-of-two block_size >= 8.  Wave w stages rows
+// [w*RW, (w+1)*RW) of the tile.  Each K load instruction covers 4 aligned rows
+// (16 lanes x 16 bytes per row) and each V load instruction 8 aligned rows
+// (lane l: rows 2*(l%4) + {0,1}, column block l/4), so the cache block
+// holding an instruction's rows is the same for the whole wave: its id is one
+// scalar load and the per-lane offsets are constant.  Same LDS layout as
+// TileLoader: K [TILE][D + 8], V^T [D][TILE + 4].
+template <int TILE, int W>
+struct PagedLoader128 {
+    static constexpr int D = 128;
+    static constexpr int KP = D + 8;
+    static constexpr int VP = TILE + 4;
+    static constexpr int ELEMS = TILE * KP + D * VP;
+    static constexpr int RW = TILE / W;     // rows per wave
+    static constexpr int KI = RW / 4;       // K load instructions per wave
+    static constexpr int VI = RW / 8;       // V load instruction pairs per wave
+    static_assert(RW % 8 == 0, "each wave stages whole 8-row groups");
+    u32x4 k[KI];
+    u32x4 v[VI][2];
+
+    // Element offset of the first row of the aligned group starting at `row0`
+    // (wave-uniform), or of page 0 when the group is past kv_limit or its
+    // page id is out of range.
+    static __device__ __forceinline__ long long group_base(const FaParams &p, const int *bt_row,
+                                                           long long head_off, int row0,
+                                                           int kv_limit) {
+        row0 = __builtin_amdgcn_readfirstlane(row0);
+        int page = row0 < kv_limit ? bt_row[row0 >> p.lbs] : 0;
+        page = __builtin_amdgcn_readfirstlane(page);
+        if (page < 0 || page >= p.num_blocks) page = 0;
+        return static_cast<long long>(page) * p.page_stride + head_off +
+               static_cast<long long>(row0 & (p.bs - 1)) * D;
+    }
+
+    __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
+                                         int j0, int kv_limit) {
+        const int lane = threadIdx.x & 63;
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int kr = lane >> 4, kc = lane & 15;          // K: row in group of 4, chunk
+        const int vr = 2 * (lane & 3), vc = lane >> 2;     // V: row pair, column block
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int row0 = j0 + w * RW + 4 * i;
+            const long long base = group_base(p, bt_row, head_off, row0, kv_limit);
+            k[i] = *reinterpret_cast<const u32x4 *>(p.kc + base + kr * D + kc * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int row0 = j0 + w * RW + 8 * i;
+            const long long base = group_base(p, bt_row, head_off, row0, kv_limit);
+            const uint16_t *src = p.vc + base + vr * D + vc * 8;
+            const u32x4 a = *reinterpret_cast<const u32x4 *>(src);
+            const u32x4 b = *reinterpret_cast<const u32x4 *>(src + D);
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            v[i][0] = row0 + vr < kv_limit ? a : zero;
+            v[i][1] = row0 + vr + 1 < kv_limit ? b : zero;
+        }
+    }
+
+    __device__ __forceinline__ void store(uint16_t *buf) const {
+        uint16_t *Ks = buf;
+        uint16_t *Vt = buf + TILE * KP;
+        const int lane = threadIdx.x & 63;
+        const int w = threadIdx.x >> 6;
+        const int kr = lane >> 4, kc = lane & 15;
+        const int vr = 2 * (lane & 3), vc = lane >> 2;
+#pragma unroll
+        for (int i = 0; i < KI; ++i)
+            *reinterpret_cast<u32x4 *>(Ks + (w * RW + 4 * i + kr) * KP + kc * 8) = k[i];
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int r = w * RW + 8 * i + vr;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // columns d = 8vc + 2e (low halves) and 8vc + 2e + 1 (high halves)
+                const uint32_t lo = __builtin_amdgcn_perm(v[i][1][e], v[i][0][e], 0x05040100u);
+                const uint32_t hi = __builtin_amdgcn_perm(v[i][1][e], v[i][0][e], 0x07060302u);
+                *reinterpret_cast<uint32_t *>(Vt + (8 * vc + 2 * e) * VP + r) = lo;
+                *reinterpret_cast<uint32_t *>(Vt + (8 * vc + 2 * e + 1) * VP + r) = hi;
+            }
+        }
+    }
+};
+
+// Loader choice: the uniform-page loader when it applies, else TileLoader.
+template <int D, int TILE, int W, bool POW2>
+struct LoaderSel {
+    using type = TileLoader<D, TILE, W * 64, POW2>;
+};
+template <int TILE, int W>
+struct LoaderSel<128, TILE, W, true> {
+    using type = PagedLoader128<TILE, W>;
+};
+
 template <typename T> struct Ones2;
 template <> struct Ones2<bf16> {
     static __device__ __forceinline__ float dot(uint32_t a, float c) {
@@ -265,7 +359,6 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
             for (int qs = 0; qs < QSUB; ++qs) s[kb][qs] = Mma<T>::run(a, qf[qs][ks], s[kb][qs]);
         }
     }
-    u32x4 pf[2 * NKB][QSUB];
 #pragma unroll
     for (int qs = 0; qs < QSUB; ++qs) {
         float mx = kNegInf;
@@ -295,23 +388,24 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
 #pragma unroll
             for (int v = 0; v < 16; ++v)
                 s[kb][qs][v] = __builtin_amdgcn_exp2f(fmaf(s[kb][qs][v], scale_log2, mneg));
-        float l = lsum[qs];
-#pragma unroll
-        for (int t = 0; t < 2 * NKB; ++t) {
-            const int kb = t >> 1, o = 8 * (t & 1);
-            pf[t][qs].x = Mma<T>::pack2(s[kb][qs][o + 0], s[kb][qs][o + 1]);
-            pf[t][qs].y = Mma<T>::pack2(s[kb][qs][o + 2], s[kb][qs][o + 3]);
-            pf[t][qs].z = Mma<T>::pack2(s[kb][qs][o + 4], s[kb][qs][o + 5]);
-            pf[t][qs].w = Mma<T>::pack2(s[kb][qs][o + 6], s[kb][qs][o + 7]);
-            l = Ones2<T>::dot(pf[t][qs].x, l);
-            l = Ones2<T>::dot(pf[t][qs].y, l);
-            l = Ones2<T>::dot(pf[t][qs].z, l);
-            l = Ones2<T>::dot(pf[t][qs].w, l);
-        }
-        lsum[qs] = l;
     }
 #pragma unroll
     for (int t = 0; t < 2 * NKB; ++t) {
+        const int kb = t >> 1, o = 8 * (t & 1);
+        u32x4 pf[QSUB];
+#pragma unroll
+        for (int qs = 0; qs < QSUB; ++qs) {
+            pf[qs].x = Mma<T>::pack2(s[kb][qs][o + 0], s[kb][qs][o + 1]);
+            pf[qs].y = Mma<T>::pack2(s[kb][qs][o + 2], s[kb][qs][o + 3]);
+            pf[qs].z = Mma<T>::pack2(s[kb][qs][o + 4], s[kb][qs][o + 5]);
+            pf[qs].w = Mma<T>::pack2(s[kb][qs][o + 6], s[kb][qs][o + 7]);
+            float l = lsum[qs];
+            l = Ones2<T>::dot(pf[qs].x, l);
+            l = Ones2<T>::dot(pf[qs].y, l);
+            l = Ones2<T>::dot(pf[qs].z, l);
+            l = Ones2<T>::dot(pf[qs].w, l);
+            lsum[qs] = l;
+        }
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) {
             const uint16_t *vr = Vt + (32 * db + r32) * VP + kv_row0 + 16 * t + 4 * g;
@@ -319,7 +413,7 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
             const u32x2 hi2 = *reinterpret_cast<const u32x2 *>(vr + 8);
             const u32x4 a = {lo2.x, lo2.y, hi2.x, hi2.y};
 #pragma unroll
-            for (int qs = 0; qs < QSUB; ++qs) oacc[qs][db] = Mma<T>::run(a, pf[t][qs], oacc[qs][db]);
+            for (int qs = 0; qs < QSUB; ++qs) oacc[qs][db] = Mma<T>::run(a, pf[qs], oacc[qs][db]);
         }
     }
 }
@@ -334,21 +428,19 @@ __device__ __forceinline__ void store_row4(uint16_t *dst, float a, float b, floa
 
 // ---------------------------------------------------------------- prefill
 
-constexpr int kPreTile = 64;
-
-template <int D>
+template <int D, int TILE>
 constexpr size_t prefill_lds_bytes() {
-    return 2 * sizeof(uint16_t) * (kPreTile * (D + 8) + D * (kPreTile + 4));
+    return 2 * sizeof(uint16_t) * (TILE * (D + 8) + D * (TILE + 4));
 }
 
 // Workgroup (b, kv head, head group, query tile) with W waves: wave w serves
 // query head hg*HW + w % HW of the GQA group and query rows
 // [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of 64 keys are double
 // buffered in LDS: one barrier per tile.
-template <typename T, int D, int W, int HW, int QSUB, bool POW2>
+template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
 __global__ void __launch_bounds__(W * 64, QSUB == 1 ? 2 : 1) fa_prefill_kernel(FaParams p) {
-    constexpr int NT = W * 64, TILE = kPreTile, NKB = TILE / 32;
-    using Loader = TileLoader<D, TILE, NT, POW2>;
+    constexpr int NKB = 2;  // keys are attended 64 at a time within a tile
+    using Loader = typename LoaderSel<D, TILE, W, POW2>::type;
     constexpr int KP = Loader::KP, VP = Loader::VP;
     constexpr int WROWS = 32 * QSUB;
     constexpr int QT = WROWS * (W / HW);
@@ -415,17 +507,20 @@ __global__ void __launch_bounds__(W * 64, QSUB == 1 ? 2 : 1) fa_prefill_kernel(F
     for (int it = 0; it < ntiles; ++it) {
         const uint16_t *cur = lds + (it & 1) * Loader::ELEMS;
         if (it + 1 < ntiles) ld.load(p, bt_row, head_off, (it + 1) * TILE, S);
-        const int j0 = it * TILE;
-        if (j0 < wave_kv_end) {
-            int lim[QSUB];
 #pragma unroll
-            for (int qs = 0; qs < QSUB; ++qs) lim[qs] = vis[qs] - j0 - 4 * g;
-            if (j0 + TILE > wave_min_vis)
-                wave_attend<T, D, KP, VP, NKB, QSUB, true>(cur, cur + TILE * KP, 0, qf, oacc, m,
-                                                           lsum, lim, p.scale_log2);
-            else
-                wave_attend<T, D, KP, VP, NKB, QSUB, false>(cur, cur + TILE * KP, 0, qf, oacc, m,
-                                                            lsum, lim, p.scale_log2);
+        for (int hb = 0; hb < TILE / 64; ++hb) {
+            const int j0 = it * TILE + 64 * hb;
+            if (j0 < wave_kv_end) {
+                int lim[QSUB];
+#pragma unroll
+                for (int qs = 0; qs < QSUB; ++qs) lim[qs] = vis[qs] - j0 - 4 * g;
+                if (j0 + 64 > wave_min_vis)
+                    wave_attend<T, D, KP, VP, NKB, QSUB, true>(cur, cur + TILE * KP, 64 * hb, qf,
+                                                               oacc, m, lsum, lim, p.scale_log2);
+                else
+                    wave_attend<T, D, KP, VP, NKB, QSUB, false>(cur, cur + TILE * KP, 64 * hb, qf,
+                                                                oacc, m, lsum, lim, p.scale_log2);
+            }
         }
         if (it + 1 < ntiles) ld.store(lds + ((it + 1) & 1) * Loader::ELEMS);
         __syncthreads();
@@ -463,7 +558,7 @@ constexpr size_t decode_lds_bytes() {
 // take the four 32-key blocks of each 128-key tile.
 template <typename T, int D, bool POW2>
 __global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
-    using Loader = TileLoader<D, kDecTile, 256, POW2>;
+    using Loader = typename LoaderSel<D, kDecTile, 4, POW2>::type;
     constexpr int KP = Loader::KP, VP = Loader::VP;
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
 
@@ -644,31 +739,33 @@ bool reserve_lds(const void *kernel, size_t bytes) {
     return true;
 }
 
-// Prefill shapes: W waves per workgroup, QSUB 32-row query blocks per wave.
-// TECOOPS_FA_PREFILL="W,QSUB" selects one of (4,1), (8,1), (4,2) for tuning.
+// Prefill shapes: W waves per workgroup, QSUB 32-row query blocks per wave,
+// TILE keys per K/V tile.  TECOOPS_FA_PREFILL="W,QSUB,TILE" selects one of
+// (8,1,64), (8,1,128), (4,1,64), (4,2,64) for tuning.
 struct PrefillCfg {
-    int w, qsub;
+    int w, qsub, tile;
 };
 
 PrefillCfg prefill_cfg() {
     static PrefillCfg cfg = [] {
-        PrefillCfg c{8, 1};
+        PrefillCfg c{8, 1, 64};
         if (const char *e = std::getenv("TECOOPS_FA_PREFILL")) {
-            int w = 0, q = 0;
-            if (std::sscanf(e, "%d,%d", &w, &q) == 2 &&
-                ((w == 4 && q == 1) || (w == 8 && q == 1) || (w == 4 && q == 2)))
-                c = PrefillCfg{w, q};
+            int w = 0, q = 0, t = 64;
+            if (std::sscanf(e, "%d,%d,%d", &w, &q, &t) >= 2 &&
+                ((w == 8 && q == 1 && (t == 64 || t == 128)) || (w == 4 && q == 1 && t == 64) ||
+                 (w == 4 && q == 2 && t == 64)))
+                c = PrefillCfg{w, q, t};
         }
         return c;
     }();
     return cfg;
 }
 
-template <typename T, int D, int W, int HW, int QSUB, bool POW2>
+template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
 tecoopsStatus_t launch_prefill(const FaParams &p, int max_q, hipStream_t s) {
     constexpr int QT = 32 * QSUB * (W / HW);
-    auto *kern = &fa_prefill_kernel<T, D, W, HW, QSUB, POW2>;
-    const size_t lds = prefill_lds_bytes<D>();
+    auto *kern = &fa_prefill_kernel<T, D, W, HW, QSUB, POW2, TILE>;
+    const size_t lds = prefill_lds_bytes<D, TILE>();
     if (!reserve_lds(reinterpret_cast<const void *>(kern), lds)) return TECOOPS_STATUS_INTERNAL_ERROR;
     dim3 grid(p.batch * p.Hkv * (p.G / HW), (max_q + QT - 1) / QT);
     hipLaunchKernelGGL(kern, grid, dim3(W * 64), lds, s, p);
@@ -676,18 +773,18 @@ tecoopsStatus_t launch_prefill(const FaParams &p, int max_q, hipStream_t s) {
     return TECOOPS_STATUS_SUCCESS;
 }
 
-template <typename T, int D, int W, int QSUB, bool POW2>
+template <typename T, int D, int W, int QSUB, bool POW2, int TILE = 64>
 tecoopsStatus_t prefill_hw(const FaParams &p, int max_q, hipStream_t s) {
     const int G = p.G;
-    if (G % 4 == 0) return launch_prefill<T, D, W, 4, QSUB, POW2>(p, max_q, s);
-    if (G % 2 == 0) return launch_prefill<T, D, W, 2, QSUB, POW2>(p, max_q, s);
-    return launch_prefill<T, D, W, 1, QSUB, POW2>(p, max_q, s);
+    if (G % 4 == 0) return launch_prefill<T, D, W, 4, QSUB, POW2, TILE>(p, max_q, s);
+    if (G % 2 == 0) return launch_prefill<T, D, W, 2, QSUB, POW2, TILE>(p, max_q, s);
+    return launch_prefill<T, D, W, 1, QSUB, POW2, TILE>(p, max_q, s);
 }
 
 template <typename T, int D>
 tecoopsStatus_t run(tecoopsHandle_t handle, FaParams &p, const Plan &pl, int max_q) {
     hipStream_t s = handle->stream;
-    const bool pow2 = p.lbs >= 0;
+    const bool pow2 = p.lbs >= 3;  // power of two and >= 8: uniform-page loader
     if (pl.decode) {
         const size_t lds = decode_lds_bytes<D>();
         auto *kern = pow2 ? &fa_decode_kernel<T, D, true> : &fa_decode_kernel<T, D, false>;
@@ -705,6 +802,7 @@ tecoopsStatus_t run(tecoopsHandle_t handle, FaParams &p, const Plan &pl, int max
                     : prefill_hw<T, D, 4, 1, false>(p, max_q, s);
     }
     const PrefillCfg c = prefill_cfg();
+    if (c.w == 8 && c.tile == 128) return prefill_hw<T, D, 8, 1, true, 128>(p, max_q, s);
     if (c.w == 8) return prefill_hw<T, D, 8, 1, true>(p, max_q, s);
     if (c.qsub == 2) return prefill_hw<T, D, 4, 2, true>(p, max_q, s);
     return prefill_hw<T, D, 4, 1, true>(p, max_q, s);
