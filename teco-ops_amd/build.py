@@ -16,6 +16,7 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "tecoops", "libtecoops.so")
+TORCH_OUT = os.path.join(HERE, "tecoops", "libtecoops_torch.so")
 
 SOURCES = [
     "handle.cpp",
@@ -52,6 +53,30 @@ def _compile(src):
     return obj, err
 
 
+def build_torch_ext(verbose=False):
+    """TORCH_LIBRARY(tecoops) registration (host C++) linked against
+    libtecoops.so; loaded with torch.ops.load_library."""
+    import torch
+    from torch.utils import cpp_extension as ce
+    inc = ce.include_paths(device_type="cuda") if "device_type" in \
+        ce.include_paths.__code__.co_varnames else ce.include_paths(cuda=True)
+    libdirs = [os.path.join(os.path.dirname(torch.__file__), "lib")]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__=1",
+           "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_EXTENSION_NAME=tecoops",
+           "-Wno-deprecated-declarations",
+           "-I", os.path.join(REPO, "include"), *sum((["-I", d] for d in inc), []),
+           os.path.join(CSRC, "torch_ext.cpp"), "-o", TORCH_OUT + ".tmp",
+           *sum((["-L", d] for d in libdirs), []),
+           "-L", os.path.dirname(OUT), "-ltecoops", "-lc10", "-lc10_hip", "-ltorch_cpu",
+           "-ltorch_hip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdirs[0]}"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"torch extension build failed:\n{' '.join(cmd)}\n{r.stderr[-4000:]}")
+    os.replace(TORCH_OUT + ".tmp", TORCH_OUT)
+    return TORCH_OUT
+
+
 def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     jobs = min(len(SOURCES), os.cpu_count() or 4, 16)
@@ -67,6 +92,7 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stderr}")
     os.replace(tmp, OUT)
+    build_torch_ext(verbose)
     return OUT
 
 

@@ -17,6 +17,7 @@ Differences from the reference wrappers, all toward its documented intent:
     transposing x and out (torch_ext.cpp:186-205).
 """
 import ctypes
+import os
 import threading
 
 import torch
@@ -24,11 +25,21 @@ import torch
 from . import _lib
 from ._lib import TecoopsError  # noqa: F401
 
+# TORCH_LIBRARY(tecoops) registrations (libtecoops_torch.so): the same ops as
+# torch.ops.tecoops.*, with torch schemas and the current-stream binding done
+# in C++.  Loaded when built; the Python functions below call the C ABI
+# directly and do not depend on it.
+_TORCH_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtecoops_torch.so")
+ops = None
+if os.path.exists(_TORCH_LIB):
+    torch.ops.load_library(_TORCH_LIB)
+    ops = torch.ops.tecoops
+
 __all__ = [
     "flatten_rays", "morton3D_invert", "reshape_and_cache", "rms_norm",
     "flash_attn_varlen_func", "causal_conv1d_fn_torch",
     # extensions
-    "rotary_embedding", "gemv", "gemv_int8", "causal_conv1d", "memset",
+    "rotary_embedding", "gemv", "gemv_int8", "causal_conv1d", "memset", "ops",
 ]
 
 _handles = {}   # device index -> [handle, bound stream]
