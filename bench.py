@@ -102,6 +102,17 @@ def build_ops(names=None):
     def want(*ns):
         return names is None or any(n in names for n in ns)
 
+    if names is not None and "copy_calibration" in names:
+        # Plain device copy of known size (opt-in): the reference point that
+        # scales rocprofv3's FETCH_SIZE / WRITE_SIZE into HBM bytes.
+        n = 256 << 20
+        fns = []
+        for _ in range(copies_for(2 * n)):
+            src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+            dst = torch.empty_like(src)
+            fns.append(lambda src=src, dst=dst: dst.copy_(src))
+        ops["copy_calibration"] = (fns, dict(bytes=2 * n))
+
     if want("rms_norm"):
         # rms_norm [4096, 4096]
         ws = 2 * 4096 * 4096 * 2
@@ -213,10 +224,11 @@ def build_ops(names=None):
     return ops
 
 
-def cpu_baseline(threads):
-    """Times the CPU oracle (C restatement of the reference's CPU paths) on one
-    (batch, kv-group) slice of the FA prefill config: 4 query heads x 4096
-    rows, causal; reported as TFLOP/s of that slice."""
+def cpu_baseline(threads, budget_s=20.0):
+    """Times the CPU oracle (C restatement of the reference's CPU paths) on the
+    FA prefill config, one (batch, kv-group) slice at a time (4 query heads x
+    4096 rows, causal): all 32 slices of the config when they fit in about
+    `budget_s` seconds, else as many as do.  Reported as TFLOP/s."""
     from oracle import oracle as orc
     if threads > 0:
         orc.set_threads(threads)
@@ -224,22 +236,32 @@ def cpu_baseline(threads):
     rng = np.random.default_rng(7)
     S, D, Hkv, H = FA_S, FA_D, FA_HKV, FA_H
     nbp = S // 16
+    G = H // Hkv
     q = orc.from_float(rng.standard_normal((S, H, D), dtype=np.float32), orc.BF16)
     kc = orc.from_float(rng.standard_normal((nbp, Hkv, 16, D), dtype=np.float32), orc.BF16)
     vc = orc.from_float(rng.standard_normal((nbp, Hkv, 16, D), dtype=np.float32), orc.BF16)
     bt = np.arange(nbp, dtype=np.int32)[None]
-    G = H // Hkv
-    flop = 4 * G * D * S * (S + 1) // 2
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        orc.flash_attention(q, kc, vc, bt, [S], [S], dtype=orc.BF16, b_only=0, h_begin=0, h_end=G)
-        times.append(time.perf_counter() - t0)
-    t = float(np.median(times))
-    return {"value": flop / t / 1e12, "unit": "TFLOP/s", "cores": used, "kind": "port",
-            "sample": f"oracle flash_attention, 1 (batch, kv-group) slice of the prefill config "
-                      f"({G} heads x {S} rows, causal, bf16 in / fp32 math), median of 3 "
-                      f"= {t:.3f} s; the full config is 32x this work",
+    slice_flop = 4 * G * D * S * (S + 1) // 2
+    done, t_total = 0, 0.0
+    for _ in range(FA_B):           # each batch of the config has the same shape
+        for g in range(Hkv):
+            t0 = time.perf_counter()
+            orc.flash_attention(q, kc, vc, bt, [S], [S], dtype=orc.BF16, b_only=0,
+                                h_begin=g * G, h_end=(g + 1) * G)
+            t_total += time.perf_counter() - t0
+            done += 1
+            if t_total >= budget_s:
+                break
+        if t_total >= budget_s:
+            break
+    total = FA_B * Hkv
+    return {"value": done * slice_flop / t_total / 1e12, "unit": "TFLOP/s", "cores": used,
+            "kind": "port",
+            "sample": f"oracle flash_attention over {done} of the {total} (batch, kv-group) slices "
+                      f"of the prefill config ({G} heads x {S} rows each, causal, bf16 in / fp32 "
+                      f"math) in {t_total:.2f} s"
+                      + ("" if done == total else
+                         f"; the full config is {total / done:.1f}x this work"),
             "cpu_model": cpu_model()}
 
 

@@ -17,6 +17,9 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "tecoops", "libtecoops.so")
 TORCH_OUT = os.path.join(HERE, "tecoops", "libtecoops_torch.so")
+PLUGIN_OUT = os.path.join(HERE, "tecoops", "libtecoops_plugin.so")
+PLUGIN_SOURCES = ["plugin/registry.cpp", "plugin/plugins.cpp"]
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 SOURCES = [
     "handle.cpp",
@@ -77,6 +80,23 @@ def build_torch_ext(verbose=False):
     return TORCH_OUT
 
 
+def build_plugins(verbose=False):
+    """Engine plugins (host C++, include/tecoops_plugin.h) linked against
+    libtecoops.so and the HIP runtime."""
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__=1",
+           "-I", os.path.join(REPO, "include"), "-I", os.path.join(ROCM, "include"),
+           *[os.path.join(CSRC, s) for s in PLUGIN_SOURCES], "-o", PLUGIN_OUT + ".tmp",
+           "-L", os.path.dirname(OUT), "-ltecoops", "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"plugin build failed:\n{' '.join(cmd)}\n{r.stderr[-4000:]}")
+    if verbose and r.stderr.strip():
+        print(r.stderr, file=sys.stderr)
+    os.replace(PLUGIN_OUT + ".tmp", PLUGIN_OUT)
+    return PLUGIN_OUT
+
+
 def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     jobs = min(len(SOURCES), os.cpu_count() or 4, 16)
@@ -92,6 +112,7 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stderr}")
     os.replace(tmp, OUT)
+    build_plugins(verbose)
     build_torch_ext(verbose)
     return OUT
 
