@@ -64,15 +64,35 @@ __device__ __forceinline__ uint32_t pack(float a, float b) {
     return static_cast<uint32_t>(Cvt<T>::from(a)) | (static_cast<uint32_t>(Cvt<T>::from(b)) << 16);
 }
 
+// Value of lane l ^ 32 combined with lane l's own, through v_permlane32_swap
+// (a VALU lane-half swap on gfx950, no LDS round trip).  With both operands
+// equal to x, the swap returns {x[l], x[l + 32]} in lanes 0-31 and
+// {x[l - 32], x[l]} in lanes 32-63.
+__device__ __forceinline__ float half_swap_max(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(r[0])),
+                 __builtin_bit_cast(float, static_cast<uint32_t>(r[1])));
+}
+
+__device__ __forceinline__ float half_swap_sum(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) +
+           __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
+    v = half_swap_sum(v);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
+    v = half_swap_max(v);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
 

@@ -25,12 +25,16 @@
 //     4-element pad) so the A operand of the PV product is two 64-bit reads.
 //     Global -> register prefetch of the next tile overlaps the current tile's
 //     MFMA work.
-//   * Prefill: a workgroup of 4 waves shares each K/V tile among up to 4 query
-//     heads of one GQA group (HW heads x (4/HW) row blocks of 32).  The grid
-//     walks query tiles heaviest-first and keeps all tiles of one (batch, kv
-//     head) on the same XCD (workgroup index % 8 depends only on (b, kv head)
-//     when B*Hkv*groups is a multiple of 8), so K/V are re-read from that
-//     XCD's L2.  MFMA-bound: 4*D*visible(q, k) FLOP per (q row, head).
+//   * Prefill (D = 128, power-of-two block_size): a workgroup of 12 waves
+//     (3 per SIMD) shares each 96-key K/V tile among up to 4 query heads of
+//     one GQA group (HW heads x (12/HW) row blocks of 32); other shapes use 4
+//     waves and 64-key tiles.  The grid walks query tiles heaviest-first and
+//     keeps all tiles of one (batch, kv head) on the same XCD (workgroup index
+//     % 8 depends only on (b, kv head) when B*Hkv*groups is a multiple of 8),
+//     so K/V are re-read from that XCD's L2.  MFMA-bound: 4*D*visible(q, k)
+//     FLOP per (q row, head).  A wave issues MFMA and VALU work serially, so
+//     the MFMA pipe is kept busy by the other waves of its SIMD: occupancy
+//     (waves per SIMD) is the main lever.
 //   * Decode (G * q_len <= 32): the 32 MFMA columns hold every (head, row) of
 //     a GQA group; 4 waves split each 128-key tile and the key range is split
 //     across workgroups (split-KV), partial (m, l, O) merged first in LDS and
@@ -160,6 +164,9 @@ struct TileLoader {
     static_assert(TILE * CPR % NT == 0 && NT % CPR == 0, "K tile must split evenly");
     u32x4 k[KCH];
     u32x4 v[VPT][4];
+    uint32_t vok;  // bit 4i+r: V row of v[i][r] is valid (below kv_limit, page in range)
+
+    __device__ __forceinline__ void prefetch(const FaParams &, const int *, int, int) {}
 
     __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
                                          int j0, int kv_limit) {
@@ -172,6 +179,9 @@ struct TileLoader {
                                                     kv_limit, ok);
             k[i] = *reinterpret_cast<const u32x4 *>(p.kc + o + col * 8);
         }
+        // Invalid V rows are zeroed in store(), so the wave does not wait for
+        // the loads here.
+        vok = 0;
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int task = tid + i * NT;
@@ -182,9 +192,8 @@ struct TileLoader {
                 bool ok;
                 const long long o = row_offset<D, POW2>(p, bt_row, head_off, j0 + 4 * rg + r,
                                                         kv_limit, ok);
-                const u32x4 x = *reinterpret_cast<const u32x4 *>(p.vc + o + cg * 8);
-                const u32x4 zero = {0u, 0u, 0u, 0u};
-                v[i][r] = ok ? x : zero;
+                v[i][r] = *reinterpret_cast<const u32x4 *>(p.vc + o + cg * 8);
+                vok |= (ok ? 1u : 0u) << (4 * i + r);
             }
         }
     }
@@ -202,7 +211,11 @@ struct TileLoader {
             const int task = tid + i * NT;
             if (VTASKS % NT != 0 && task >= VTASKS) continue;
             const int rg = task % (TILE / 4), cg = task / (TILE / 4);
-            const u32x4 a = v[i][0], b = v[i][1], c = v[i][2], d = v[i][3];
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            const u32x4 a = (vok >> (4 * i)) & 1u ? v[i][0] : zero;
+            const u32x4 b = (vok >> (4 * i + 1)) & 1u ? v[i][1] : zero;
+            const u32x4 c = (vok >> (4 * i + 2)) & 1u ? v[i][2] : zero;
+            const u32x4 d = (vok >> (4 * i + 3)) & 1u ? v[i][3] : zero;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 // columns d = 8cg + 2w (low halves) and 8cg + 2w + 1 (high halves)
@@ -222,9 +235,11 @@ struct TileLoader {
 // [w*RW, (w+1)*RW) of the tile.  Each K load instruction covers 4 aligned rows
 // (16 lanes x 16 bytes per row) and each V load instruction 8 aligned rows
 // (lane l: rows 2*(l%4) + {0,1}, column block l/4), so the cache block
-// holding an instruction's rows is the same for the whole wave: its id is one
-// scalar load and the per-lane offsets are constant.  Same LDS layout as
-// TileLoader: K [TILE][D + 8], V^T [D][TILE + 4].
+// holding an instruction's rows is the same for the whole wave: its id is a
+// scalar, read from the block table one load() call ahead (prefetch), so the
+// global loads never wait for it.  Same LDS layout as TileLoader: K [TILE][D +
+// 8], V^T [D][TILE + 4].  load() must be called for consecutive tiles after
+// one prefetch() of the first.
 template <int TILE, int W>
 struct PagedLoader128 {
     static constexpr int D = 128;
@@ -237,19 +252,34 @@ struct PagedLoader128 {
     static_assert(RW % 8 == 0, "each wave stages whole 8-row groups");
     u32x4 k[KI];
     u32x4 v[VI][2];
+    uint32_t vok;     // bit 2i+j: V row of v[i][j] is below kv_limit
+    int pg[KI + VI];  // cache block ids of the next load()'s row groups (uniform)
 
-    // Element offset of the first row of the aligned group starting at `row0`
-    // (wave-uniform), or of page 0 when the group is past kv_limit or its
-    // page id is out of range.
-    static __device__ __forceinline__ long long group_base(const FaParams &p, const int *bt_row,
-                                                           long long head_off, int row0,
-                                                           int kv_limit) {
+    // Block id of the aligned row group starting at `row0` (wave-uniform), or
+    // 0 past kv_limit.
+    static __device__ __forceinline__ int group_page(const FaParams &p, const int *bt_row,
+                                                     int row0, int kv_limit) {
         row0 = __builtin_amdgcn_readfirstlane(row0);
-        int page = row0 < kv_limit ? bt_row[row0 >> p.lbs] : 0;
-        page = __builtin_amdgcn_readfirstlane(page);
+        const int page = row0 < kv_limit ? bt_row[row0 >> p.lbs] : 0;
+        return __builtin_amdgcn_readfirstlane(page);
+    }
+
+    // Element offset of the group's first row (page 0 when its id is out of range).
+    static __device__ __forceinline__ long long group_base(const FaParams &p, long long head_off,
+                                                           int row0, int page) {
         if (page < 0 || page >= p.num_blocks) page = 0;
         return static_cast<long long>(page) * p.page_stride + head_off +
                static_cast<long long>(row0 & (p.bs - 1)) * D;
+    }
+
+    __device__ __forceinline__ void prefetch(const FaParams &p, const int *bt_row, int j0,
+                                             int kv_limit) {
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < KI; ++i) pg[i] = group_page(p, bt_row, j0 + w * RW + 4 * i, kv_limit);
+#pragma unroll
+        for (int i = 0; i < VI; ++i)
+            pg[KI + i] = group_page(p, bt_row, j0 + w * RW + 8 * i, kv_limit);
     }
 
     __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
@@ -261,20 +291,23 @@ struct PagedLoader128 {
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int row0 = j0 + w * RW + 4 * i;
-            const long long base = group_base(p, bt_row, head_off, row0, kv_limit);
+            const long long base = group_base(p, head_off, row0, pg[i]);
             k[i] = *reinterpret_cast<const u32x4 *>(p.kc + base + kr * D + kc * 8);
         }
+        // V rows at or past kv_limit are zeroed in store(), not here: a select
+        // on the loaded value would make the wave wait for the load at once.
+        vok = 0;
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
             const int row0 = j0 + w * RW + 8 * i;
-            const long long base = group_base(p, bt_row, head_off, row0, kv_limit);
+            const long long base = group_base(p, head_off, row0, pg[KI + i]);
             const uint16_t *src = p.vc + base + vr * D + vc * 8;
-            const u32x4 a = *reinterpret_cast<const u32x4 *>(src);
-            const u32x4 b = *reinterpret_cast<const u32x4 *>(src + D);
-            const u32x4 zero = {0u, 0u, 0u, 0u};
-            v[i][0] = row0 + vr < kv_limit ? a : zero;
-            v[i][1] = row0 + vr + 1 < kv_limit ? b : zero;
+            v[i][0] = *reinterpret_cast<const u32x4 *>(src);
+            v[i][1] = *reinterpret_cast<const u32x4 *>(src + D);
+            vok |= (row0 + vr < kv_limit ? 1u : 0u) << (2 * i);
+            vok |= (row0 + vr + 1 < kv_limit ? 1u : 0u) << (2 * i + 1);
         }
+        prefetch(p, bt_row, j0 + TILE, kv_limit);
     }
 
     __device__ __forceinline__ void store(uint16_t *buf) const {
@@ -290,11 +323,14 @@ struct PagedLoader128 {
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
             const int r = w * RW + 8 * i + vr;
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            const u32x4 a = (vok >> (2 * i)) & 1u ? v[i][0] : zero;
+            const u32x4 b = (vok >> (2 * i + 1)) & 1u ? v[i][1] : zero;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 // columns d = 8vc + 2e (low halves) and 8vc + 2e + 1 (high halves)
-                const uint32_t lo = __builtin_amdgcn_perm(v[i][1][e], v[i][0][e], 0x05040100u);
-                const uint32_t hi = __builtin_amdgcn_perm(v[i][1][e], v[i][0][e], 0x07060302u);
+                const uint32_t lo = __builtin_amdgcn_perm(b[e], a[e], 0x05040100u);
+                const uint32_t hi = __builtin_amdgcn_perm(b[e], a[e], 0x07060302u);
                 *reinterpret_cast<uint32_t *>(Vt + (8 * vc + 2 * e) * VP + r) = lo;
                 *reinterpret_cast<uint32_t *>(Vt + (8 * vc + 2 * e + 1) * VP + r) = hi;
             }
@@ -361,7 +397,8 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
     }
 #pragma unroll
     for (int qs = 0; qs < QSUB; ++qs) {
-        float mx = kNegInf;
+        // masked scores, then their max as a tree (short dependency chain)
+        float t4[NKB * 4];
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -369,9 +406,19 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
                 float x = s[kb][qs][v];
                 if (MASK && !(32 * kb + 8 * (v >> 2) + (v & 3) < lim[qs])) x = kNegInf;
                 s[kb][qs][v] = x;
-                mx = fmaxf(mx, x);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                t4[kb * 4 + u] = fmaxf(fmaxf(s[kb][qs][4 * u], s[kb][qs][4 * u + 1]),
+                                       fmaxf(s[kb][qs][4 * u + 2], s[kb][qs][4 * u + 3]));
+#pragma unroll
+        for (int w = NKB * 4; w > 1; w >>= 1)
+#pragma unroll
+            for (int u = 0; u < w / 2; ++u) t4[u] = fmaxf(t4[u], t4[u + w / 2]);
+        float mx = t4[0];
+        mx = half_swap_max(mx) * scale_log2;
         if (!__all(mx <= m[qs] + kRescaleSlack)) {
             const float m_new = fmaxf(m[qs], mx);  // m >= 0 keeps the reference clamp
             const float alpha = __builtin_amdgcn_exp2f(m[qs] - m_new);
@@ -435,11 +482,15 @@ constexpr size_t prefill_lds_bytes() {
 
 // Workgroup (b, kv head, head group, query tile) with W waves: wave w serves
 // query head hg*HW + w % HW of the GQA group and query rows
-// [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of 64 keys are double
-// buffered in LDS: one barrier per tile.
+// [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of TILE keys are double
+// buffered in LDS (one barrier per tile) and attended 32 * NKB keys at a time.
+// W >= 12 asks for 3 waves per SIMD (168 VGPRs), else 2.
 template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
-__global__ void __launch_bounds__(W * 64, QSUB == 1 ? 2 : 1) fa_prefill_kernel(FaParams p) {
-    constexpr int NKB = 2;  // keys are attended 64 at a time within a tile
+__global__ void __launch_bounds__(W * 64, W >= 12 ? 3 : 2)
+fa_prefill_kernel(FaParams p) {
+    // keys are attended 32 * NKB at a time within a tile
+    constexpr int NKB = TILE % 64 == 0 ? 2 : 1;
+    constexpr int KB = 32 * NKB;
     using Loader = typename LoaderSel<D, TILE, W, POW2>::type;
     constexpr int KP = Loader::KP, VP = Loader::VP;
     constexpr int WROWS = 32 * QSUB;
@@ -500,6 +551,7 @@ __global__ void __launch_bounds__(W * 64, QSUB == 1 ? 2 : 1) fa_prefill_kernel(F
     Loader ld;
     const int ntiles = (kv_end + TILE - 1) / TILE;
     if (ntiles > 0) {
+        ld.prefetch(p, bt_row, 0, S);
         ld.load(p, bt_row, head_off, 0, S);
         ld.store(lds);
     }
@@ -508,17 +560,17 @@ __global__ void __launch_bounds__(W * 64, QSUB == 1 ? 2 : 1) fa_prefill_kernel(F
         const uint16_t *cur = lds + (it & 1) * Loader::ELEMS;
         if (it + 1 < ntiles) ld.load(p, bt_row, head_off, (it + 1) * TILE, S);
 #pragma unroll
-        for (int hb = 0; hb < TILE / 64; ++hb) {
-            const int j0 = it * TILE + 64 * hb;
+        for (int hb = 0; hb < TILE / KB; ++hb) {
+            const int j0 = it * TILE + KB * hb;
             if (j0 < wave_kv_end) {
                 int lim[QSUB];
 #pragma unroll
                 for (int qs = 0; qs < QSUB; ++qs) lim[qs] = vis[qs] - j0 - 4 * g;
-                if (j0 + 64 > wave_min_vis)
-                    wave_attend<T, D, KP, VP, NKB, QSUB, true>(cur, cur + TILE * KP, 64 * hb, qf,
+                if (j0 + KB > wave_min_vis)
+                    wave_attend<T, D, KP, VP, NKB, QSUB, true>(cur, cur + TILE * KP, KB * hb, qf,
                                                                oacc, m, lsum, lim, p.scale_log2);
                 else
-                    wave_attend<T, D, KP, VP, NKB, QSUB, false>(cur, cur + TILE * KP, 64 * hb, qf,
+                    wave_attend<T, D, KP, VP, NKB, QSUB, false>(cur, cur + TILE * KP, KB * hb, qf,
                                                                 oacc, m, lsum, lim, p.scale_log2);
             }
         }
@@ -528,7 +580,7 @@ __global__ void __launch_bounds__(W * 64, QSUB == 1 ? 2 : 1) fa_prefill_kernel(F
 
 #pragma unroll
     for (int qs = 0; qs < QSUB; ++qs) {
-        const float lt = lsum[qs] + __shfl_xor(lsum[qs], 32, 64);
+        const float lt = half_swap_sum(lsum[qs]);
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
         const int row = qw0 + 32 * qs + r32;
         if (row < L) {
@@ -604,7 +656,10 @@ __global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
 
     Loader ld;
     const int ntiles = (kv_hi - kv_lo + kDecTile - 1) / kDecTile;
-    if (ntiles > 0) ld.load(p, bt_row, head_off, kv_lo, kv_hi);
+    if (ntiles > 0) {
+        ld.prefetch(p, bt_row, kv_lo, kv_hi);
+        ld.load(p, bt_row, head_off, kv_lo, kv_hi);
+    }
     for (int it = 0; it < ntiles; ++it) {
         const int j0 = kv_lo + it * kDecTile;
         __syncthreads();
@@ -628,7 +683,7 @@ __global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
     float *lm = reinterpret_cast<float *>(smem);   // [4][32] max
     float *ll = lm + 4 * 32;                        // [4][32] sum
     float *lo = ll + 4 * 32;                        // [4][32][D] unnormalised O
-    const float lt = lsum[0] + __shfl_xor(lsum[0], 32, 64);
+    const float lt = half_swap_sum(lsum[0]);
     if (g == 0) {
         lm[wave * 32 + r32] = m[0];
         ll[wave * 32 + r32] = lt;
@@ -739,22 +794,21 @@ bool reserve_lds(const void *kernel, size_t bytes) {
     return true;
 }
 
-// Prefill shapes: W waves per workgroup, QSUB 32-row query blocks per wave,
-// TILE keys per K/V tile.  TECOOPS_FA_PREFILL="W,QSUB,TILE" selects one of
-// (8,1,64), (8,1,128), (4,1,64), (4,2,64) for tuning.
+// Prefill shape: W waves per workgroup and TILE keys per K/V tile.
 struct PrefillCfg {
-    int w, qsub, tile;
+    int w, tile;
 };
 
+// Prefill variant for D = 128 with the uniform-page loader: 12 waves (3 per
+// SIMD) and 96-key tiles by default; TECOOPS_FA_PREFILL="8,1,64" selects the
+// 8-wave, 64-key-tile variant (A/B measurements).
 PrefillCfg prefill_cfg() {
     static PrefillCfg cfg = [] {
-        PrefillCfg c{8, 1, 64};
+        PrefillCfg c{12, 96};
         if (const char *e = std::getenv("TECOOPS_FA_PREFILL")) {
-            int w = 0, q = 0, t = 64;
-            if (std::sscanf(e, "%d,%d,%d", &w, &q, &t) >= 2 &&
-                ((w == 8 && q == 1 && (t == 64 || t == 128)) || (w == 4 && q == 1 && t == 64) ||
-                 (w == 4 && q == 2 && t == 64)))
-                c = PrefillCfg{w, q, t};
+            int w = 0, q = 0, t = 0;
+            if (std::sscanf(e, "%d,%d,%d", &w, &q, &t) == 3 && w == 8 && q == 1 && t == 64)
+                c = PrefillCfg{8, 64};
         }
         return c;
     }();
@@ -802,10 +856,8 @@ tecoopsStatus_t run(tecoopsHandle_t handle, FaParams &p, const Plan &pl, int max
                     : prefill_hw<T, D, 4, 1, false>(p, max_q, s);
     }
     const PrefillCfg c = prefill_cfg();
-    if (c.w == 8 && c.tile == 128) return prefill_hw<T, D, 8, 1, true, 128>(p, max_q, s);
-    if (c.w == 8) return prefill_hw<T, D, 8, 1, true>(p, max_q, s);
-    if (c.qsub == 2) return prefill_hw<T, D, 4, 2, true>(p, max_q, s);
-    return prefill_hw<T, D, 4, 1, true>(p, max_q, s);
+    if (c.w == 8) return prefill_hw<T, D, 8, 1, true, 64>(p, max_q, s);
+    return prefill_hw<T, D, 12, 1, true, 96>(p, max_q, s);
 }
 
 bool is_packed_rowmajor(const tecoopsTensorStruct *d) {
