@@ -8,6 +8,8 @@ inputs already resident in HBM (synthetic seeded data):
   reshape_cache   key/value fp16 [8192, 8, 128] -> 1024 blocks x 16 slots
   causal_conv1d   x fp16 [8, 4096, 2048], width 4, bias, SiLU, final state
   rotary          q [8192, 32, 128], k [8192, 8, 128], neox, base 1e4
+  rotary_cache    the fused decode step: rotary on q, k [8192, 8, 128] and
+                  k, v into 1024 blocks x 16 (rotary + reshape_and_cache)
   gemv_f16_b{1,8} W fp16 [14336, 4096]
   gemv_i8_b{1,8}  W int8 [14336, 4096] + fp16 scales
   fa_prefill      bf16 q [4, 32, 4096, 128], k/v [4, 8, 4096, 128], causal
@@ -164,6 +166,24 @@ def build_ops(names=None):
             k = seeded_bits(rng, (8192, 8, 128))
             fns.append(lambda q=q, k=k: tecoops.rotary_embedding(pos, q, k, 128))
         ops["rotary"] = (fns, dict(bytes=2 * (8192 * 40 * 128) * 2 + 8192 * 8))
+
+    if want("rotary_cache"):
+        # fused decode step: rotary on q (in place) and k, k and v into the
+        # paged cache (rotary + reshape_and_cache configs as one pass)
+        T, H, Hkv, D, NB, BS = 8192, 32, 8, 128, 1024, 16
+        ws = 2 * T * H * D * 2 + 4 * T * Hkv * D * 2
+        pos = torch.from_numpy((np.arange(T) % 2048).astype(np.int64)).cuda()
+        slots = torch.from_numpy(rng.permutation(NB * BS)[:T].astype(np.int64)).cuda()
+        fns = []
+        for _ in range(copies_for(ws)):
+            q = seeded_bits(rng, (T, H, D))
+            k = seeded_bits(rng, (T, Hkv, D))
+            v = seeded_bits(rng, (T, Hkv, D))
+            kc = torch.zeros((NB, Hkv, BS, D), dtype=torch.float16, device="cuda")
+            vc = torch.zeros_like(kc)
+            fns.append(lambda q=q, k=k, v=v, kc=kc, vc=vc: tecoops.rotary_reshape_and_cache(
+                pos, q, k, v, slots, kc, vc, D))
+        ops["rotary_cache"] = (fns, dict(bytes=ws + 2 * T * 8))
 
     if want("gemv_f16_b1", "gemv_f16_b8", "gemv_i8_b1", "gemv_i8_b8"):
         # GEMV: W fp16 / int8 [14336, 4096]

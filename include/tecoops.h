@@ -272,6 +272,26 @@ tecoopsStatus_t tecoopsRotaryEmbedding(tecoopsHandle_t handle, const int64_t *po
                                        const float *cos_sin_cache, int max_position,
                                        float base, int is_neox, tecoopsDataType_t dataType);
 
+/* Fused decode step over the paged KV cache: rotary embedding on query (in
+ * place) and key as tecoopsRotaryEmbedding, then the rotated key and value
+ * [num_tokens, num_kv_heads, head_size] (token stride value_stride) stored at
+ * slot_mapping[t] of key_cache / value_cache [num_blocks, num_kv_heads,
+ * block_size, head_size] as tecoopsReshapeAndCache (slots < 0 or past the
+ * cache are not stored).  write_key != 0 also writes the rotated key back in
+ * place.  The cached values are bit-identical to those two calls in sequence. */
+tecoopsStatus_t tecoopsRotaryReshapeAndCache(tecoopsHandle_t handle, const int64_t *positions,
+                                             void *query, void *key, const void *value,
+                                             const int64_t *slot_mapping,
+                                             void *key_cache, void *value_cache,
+                                             int num_tokens, int num_heads, int num_kv_heads,
+                                             int head_size, int rot_dim,
+                                             long long query_stride, long long key_stride,
+                                             long long value_stride,
+                                             const float *cos_sin_cache, int max_position,
+                                             float base, int is_neox,
+                                             int num_blocks, int block_size, int write_key,
+                                             tecoopsDataType_t dataType);
+
 /* y[b, n] = sum_k W[n, k] * x[b, k], fp32 accumulation.
  * W [n, k] row-major, x [batch, k], y [batch, n]; dataType HALF or BFLOAT16. */
 tecoopsStatus_t tecoopsGemv(tecoopsHandle_t handle, const void *weight, const void *x, void *y,

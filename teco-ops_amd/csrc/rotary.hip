@@ -23,6 +23,47 @@ constexpr int kMaxHalf = 256;  // rot_dim <= 512
 
 constexpr int kTokensPerBlock = 4;
 
+// Rotation of 4 NeoX pairs (x1 = a, x2 = b, 4 elements each, as 8-byte words)
+// with (cos, sin) c[0..3]: o1 = x1 cos - x2 sin, o2 = x2 cos + x1 sin.
+template <typename T>
+__device__ __forceinline__ void rot_neox4(const uint2 &a, const uint2 &b, const float2 *c,
+                                          uint2 &oa, uint2 &ob) {
+    const uint32_t pa[2] = {a.x, a.y}, pb[2] = {b.x, b.y};
+    uint32_t qa[2], qb[2];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const float2 c0 = c[2 * w], c1 = c[2 * w + 1];
+        const float x10 = lo<T>(pa[w]), x11 = hi<T>(pa[w]);
+        const float x20 = lo<T>(pb[w]), x21 = hi<T>(pb[w]);
+        qa[w] = pack<T>(x10 * c0.x - x20 * c0.y, x11 * c1.x - x21 * c1.y);
+        qb[w] = pack<T>(x20 * c0.x + x10 * c0.y, x21 * c1.x + x11 * c1.y);
+    }
+    oa = make_uint2(qa[0], qa[1]);
+    ob = make_uint2(qb[0], qb[1]);
+}
+
+// Rotation of 4 adjacent GPT-J pairs packed in 16 bytes.
+template <typename T>
+__device__ __forceinline__ uint4 rot_gptj4(const uint4 &a, const float2 *c) {
+    uint32_t pa[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float2 cc = c[w];
+        const float x1 = lo<T>(pa[w]), x2 = hi<T>(pa[w]);
+        pa[w] = pack<T>(x1 * cc.x - x2 * cc.y, x2 * cc.x + x1 * cc.y);
+    }
+    return make_uint4(pa[0], pa[1], pa[2], pa[3]);
+}
+
+// One pair, scalar.
+template <typename T>
+__device__ __forceinline__ void rot_pair(uint16_t x1b, uint16_t x2b, float2 cc, uint16_t &o1,
+                                         uint16_t &o2) {
+    const float x1 = Cvt<T>::to(x1b), x2 = Cvt<T>::to(x2b);
+    o1 = Cvt<T>::from(x1 * cc.x - x2 * cc.y);
+    o2 = Cvt<T>::from(x2 * cc.x + x1 * cc.y);
+}
+
 template <typename T, bool NEOX, bool VEC>
 __global__ void __launch_bounds__(kThreads)
 rotary_kernel(const int64_t *__restrict__ positions, uint16_t *__restrict__ query,
@@ -79,47 +120,200 @@ rotary_kernel(const int64_t *__restrict__ positions, uint16_t *__restrict__ quer
             if (VEC) {
                 uint2 *p1 = reinterpret_cast<uint2 *>(row + i0);
                 uint2 *p2 = reinterpret_cast<uint2 *>(row + half + i0);
-                uint2 a = *p1, b = *p2;
-                const uint32_t *pa = reinterpret_cast<const uint32_t *>(&a);
-                const uint32_t *pb = reinterpret_cast<const uint32_t *>(&b);
                 uint2 oa, ob;
-                uint32_t *qa = reinterpret_cast<uint32_t *>(&oa);
-                uint32_t *qb = reinterpret_cast<uint32_t *>(&ob);
-#pragma unroll
-                for (int w = 0; w < 2; ++w) {
-                    const float2 c0 = c[i0 + 2 * w], c1 = c[i0 + 2 * w + 1];
-                    const float x10 = lo<T>(pa[w]), x11 = hi<T>(pa[w]);
-                    const float x20 = lo<T>(pb[w]), x21 = hi<T>(pb[w]);
-                    qa[w] = pack<T>(x10 * c0.x - x20 * c0.y, x11 * c1.x - x21 * c1.y);
-                    qb[w] = pack<T>(x20 * c0.x + x10 * c0.y, x21 * c1.x + x11 * c1.y);
-                }
+                rot_neox4<T>(*p1, *p2, c + i0, oa, ob);
                 *p1 = oa;
                 *p2 = ob;
             } else {
-                const float2 cc = c[i0];
-                const float x1 = Cvt<T>::to(row[i0]), x2 = Cvt<T>::to(row[half + i0]);
-                row[i0] = Cvt<T>::from(x1 * cc.x - x2 * cc.y);
-                row[half + i0] = Cvt<T>::from(x2 * cc.x + x1 * cc.y);
+                rot_pair<T>(row[i0], row[half + i0], c[i0], row[i0], row[half + i0]);
             }
         } else {
             if (VEC) {
-                uint4 *p = reinterpret_cast<uint4 *>(row + 2 * i0);
-                uint4 a = *p;
-                uint32_t *pa = reinterpret_cast<uint32_t *>(&a);
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const float2 cc = c[i0 + w];
-                    const float x1 = lo<T>(pa[w]), x2 = hi<T>(pa[w]);
-                    pa[w] = pack<T>(x1 * cc.x - x2 * cc.y, x2 * cc.x + x1 * cc.y);
-                }
-                *p = a;
+                uint4 *pp = reinterpret_cast<uint4 *>(row + 2 * i0);
+                *pp = rot_gptj4<T>(*pp, c + i0);
             } else {
-                const float2 cc = c[i0];
-                const float x1 = Cvt<T>::to(row[2 * i0]), x2 = Cvt<T>::to(row[2 * i0 + 1]);
-                row[2 * i0] = Cvt<T>::from(x1 * cc.x - x2 * cc.y);
-                row[2 * i0 + 1] = Cvt<T>::from(x2 * cc.x + x1 * cc.y);
+                rot_pair<T>(row[2 * i0], row[2 * i0 + 1], c[i0], row[2 * i0], row[2 * i0 + 1]);
             }
         }
+    }
+}
+
+// Fused decode-step kernel: rotary on query (in place) and key, rotated key
+// and value written straight into the paged caches [num_blocks, Hkv,
+// block_size, D] at slot_mapping[t] (key also written back in place when
+// write_key).  Same cos / sin and rotation arithmetic as rotary_kernel, so the
+// cache holds exactly what rotary_embedding followed by reshape_and_cache
+// would store.  A token whose position is outside the cos/sin cache is not
+// rotated (identity), as in rotary_kernel, but is still cached; slots < 0 or
+// >= num_blocks * block_size are not cached, as in reshape_and_cache.
+struct FusedArgs {
+    const int64_t *positions;
+    uint16_t *query;
+    uint16_t *key;
+    const uint16_t *value;
+    const int64_t *slots;
+    uint16_t *kcache;
+    uint16_t *vcache;
+    int num_tokens, num_heads, num_kv_heads, head_size, rot_dim;
+    long long q_stride, k_stride, v_stride;
+    const float *cos_sin_cache;
+    int max_position;
+    float log2_base;
+    int block_size, lbs;  // lbs = log2(block_size) or -1
+    long long capacity;   // num_blocks * block_size
+    int write_key;
+};
+
+template <typename T, bool NEOX, bool VEC>
+__global__ void __launch_bounds__(kThreads) rotary_cache_kernel(FusedArgs a) {
+    __shared__ float2 cs[kTokensPerBlock][kMaxHalf];
+    __shared__ long long crow[kTokensPerBlock];  // first element of the token's cache row, or -1
+    const int half = a.rot_dim >> 1;
+    const int D = a.head_size;
+    const int tbase = blockIdx.x * kTokensPerBlock;
+    for (int e = threadIdx.x; e < kTokensPerBlock * half; e += blockDim.x) {
+        const int tt = e / half, i = e - tt * half;
+        const int t = tbase + tt;
+        if (t >= a.num_tokens) continue;
+        const int64_t pos = a.positions[t];
+        float c = 1.0f, sn = 0.0f;
+        if (a.cos_sin_cache != nullptr) {
+            if (pos >= 0 && pos < a.max_position) {
+                c = a.cos_sin_cache[pos * a.rot_dim + i];
+                sn = a.cos_sin_cache[pos * a.rot_dim + half + i];
+            }
+        } else {
+            const float inv_freq = exp2f(-(2.0f * i / static_cast<float>(a.rot_dim)) * a.log2_base);
+            sincosf(static_cast<float>(pos) * inv_freq, &sn, &c);
+        }
+        cs[tt][i] = make_float2(c, sn);
+    }
+    if (threadIdx.x < kTokensPerBlock) {
+        const int t = tbase + threadIdx.x;
+        long long r = -1;
+        if (t < a.num_tokens) {
+            const int64_t slot = a.slots[t];
+            if (slot >= 0 && slot < a.capacity) {
+                const int s32 = static_cast<int>(slot);
+                const int blk = a.lbs >= 0 ? s32 >> a.lbs : s32 / a.block_size;
+                const int off = a.lbs >= 0 ? s32 & (a.block_size - 1) : s32 - blk * a.block_size;
+                r = (static_cast<long long>(blk) * a.num_kv_heads * a.block_size + off) * D;
+            }
+        }
+        crow[threadIdx.x] = r;
+    }
+    __syncthreads();
+    constexpr int P = VEC ? 4 : 1;        // rotation pairs per task
+    constexpr int CV = VEC ? 8 : 1;       // elements per copy task
+    const int rot_tasks = half / P;       // per head
+    const int tail = D - a.rot_dim;       // key elements past rot_dim: copied unrotated
+    const int tail_tasks = (tail + CV - 1) / CV;
+    const int v_tasks = D / CV;
+    const int nq = a.num_heads * rot_tasks;
+    const int nk = a.num_kv_heads * (rot_tasks + tail_tasks);
+    const int per_token = nq + nk + a.num_kv_heads * v_tasks;
+    const long long head_stride = static_cast<long long>(a.block_size) * D;  // cache, per kv head
+    for (int task = threadIdx.x; task < kTokensPerBlock * per_token; task += blockDim.x) {
+        const int tt = task / per_token;
+        const int t = tbase + tt;
+        if (t >= a.num_tokens) continue;
+        int local = task - tt * per_token;
+        const float2 *c = cs[tt];
+        const long long cr = crow[tt];
+        if (local < nq) {  // query head: rotate in place
+            const int h = local / rot_tasks;
+            const int i0 = (local - h * rot_tasks) * P;
+            uint16_t *row = a.query + t * a.q_stride + h * D;
+            if (NEOX) {
+                if (VEC) {
+                    uint2 *p1 = reinterpret_cast<uint2 *>(row + i0);
+                    uint2 *p2 = reinterpret_cast<uint2 *>(row + half + i0);
+                    uint2 oa, ob;
+                    rot_neox4<T>(*p1, *p2, c + i0, oa, ob);
+                    *p1 = oa;
+                    *p2 = ob;
+                } else {
+                    rot_pair<T>(row[i0], row[half + i0], c[i0], row[i0], row[half + i0]);
+                }
+            } else {
+                if (VEC) {
+                    uint4 *pp = reinterpret_cast<uint4 *>(row + 2 * i0);
+                    *pp = rot_gptj4<T>(*pp, c + i0);
+                } else {
+                    rot_pair<T>(row[2 * i0], row[2 * i0 + 1], c[i0], row[2 * i0], row[2 * i0 + 1]);
+                }
+            }
+            continue;
+        }
+        local -= nq;
+        if (local < nk) {  // key head: rotate, then cache (and write back)
+            const int per_head = rot_tasks + tail_tasks;
+            const int h = local / per_head;
+            const int r = local - h * per_head;
+            uint16_t *row = a.key + t * a.k_stride + h * D;
+            uint16_t *dst = cr >= 0 ? a.kcache + cr + h * head_stride : nullptr;
+            if (r >= rot_tasks) {  // unrotated tail
+                const int e0 = a.rot_dim + (r - rot_tasks) * CV;
+                if (dst != nullptr)
+                    for (int e = e0; e < e0 + CV && e < D; ++e) dst[e] = row[e];
+                continue;
+            }
+            const int i0 = r * P;
+            if (NEOX) {
+                if (VEC) {
+                    uint2 oa, ob;
+                    rot_neox4<T>(*reinterpret_cast<const uint2 *>(row + i0),
+                                 *reinterpret_cast<const uint2 *>(row + half + i0), c + i0, oa, ob);
+                    if (a.write_key) {
+                        *reinterpret_cast<uint2 *>(row + i0) = oa;
+                        *reinterpret_cast<uint2 *>(row + half + i0) = ob;
+                    }
+                    if (dst != nullptr) {
+                        *reinterpret_cast<uint2 *>(dst + i0) = oa;
+                        *reinterpret_cast<uint2 *>(dst + half + i0) = ob;
+                    }
+                } else {
+                    uint16_t o1, o2;
+                    rot_pair<T>(row[i0], row[half + i0], c[i0], o1, o2);
+                    if (a.write_key) {
+                        row[i0] = o1;
+                        row[half + i0] = o2;
+                    }
+                    if (dst != nullptr) {
+                        dst[i0] = o1;
+                        dst[half + i0] = o2;
+                    }
+                }
+            } else {
+                if (VEC) {
+                    const uint4 o = rot_gptj4<T>(*reinterpret_cast<const uint4 *>(row + 2 * i0), c + i0);
+                    if (a.write_key) *reinterpret_cast<uint4 *>(row + 2 * i0) = o;
+                    if (dst != nullptr) *reinterpret_cast<uint4 *>(dst + 2 * i0) = o;
+                } else {
+                    uint16_t o1, o2;
+                    rot_pair<T>(row[2 * i0], row[2 * i0 + 1], c[i0], o1, o2);
+                    if (a.write_key) {
+                        row[2 * i0] = o1;
+                        row[2 * i0 + 1] = o2;
+                    }
+                    if (dst != nullptr) {
+                        dst[2 * i0] = o1;
+                        dst[2 * i0 + 1] = o2;
+                    }
+                }
+            }
+            continue;
+        }
+        local -= nk;
+        if (cr < 0) continue;  // value head: copy into the cache
+        const int h = local / v_tasks;
+        const int e0 = (local - h * v_tasks) * CV;
+        const uint16_t *src = a.value + t * a.v_stride + h * D + e0;
+        uint16_t *dst = a.vcache + cr + h * head_stride + e0;
+        if (VEC)
+            *reinterpret_cast<uint4 *>(dst) = *reinterpret_cast<const uint4 *>(src);
+        else
+            *dst = *src;
     }
 }
 
@@ -189,5 +383,81 @@ extern "C" tecoopsStatus_t tecoopsRotaryEmbedding(tecoopsHandle_t handle,
                                  max_position, lb);
     }
     TECO_CHECK_LAUNCH("rotary_embedding");
+    return TECOOPS_STATUS_SUCCESS;
+}
+
+extern "C" tecoopsStatus_t tecoopsRotaryReshapeAndCache(
+    tecoopsHandle_t handle, const int64_t *positions, void *query, void *key, const void *value,
+    const int64_t *slot_mapping, void *key_cache, void *value_cache, int num_tokens,
+    int num_heads, int num_kv_heads, int head_size, int rot_dim, long long query_stride,
+    long long key_stride, long long value_stride, const float *cos_sin_cache, int max_position,
+    float base, int is_neox, int num_blocks, int block_size, int write_key,
+    tecoopsDataType_t dataType) {
+    if (handle == nullptr) return TECOOPS_STATUS_NOT_INITIALIZED;
+    if (positions == nullptr || query == nullptr || key == nullptr || value == nullptr ||
+        slot_mapping == nullptr || key_cache == nullptr || value_cache == nullptr)
+        return TECOOPS_STATUS_BAD_PARAM;
+    if (num_tokens <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 ||
+        num_blocks <= 0 || block_size <= 0)
+        return TECOOPS_STATUS_BAD_PARAM;
+    if (rot_dim <= 0 || (rot_dim & 1) || rot_dim > head_size || rot_dim / 2 > kMaxHalf)
+        return TECOOPS_STATUS_BAD_PARAM;
+    if (query_stride < static_cast<long long>(num_heads) * head_size ||
+        key_stride < static_cast<long long>(num_kv_heads) * head_size ||
+        value_stride < static_cast<long long>(num_kv_heads) * head_size)
+        return TECOOPS_STATUS_BAD_PARAM;
+    if (cos_sin_cache != nullptr && max_position <= 0) return TECOOPS_STATUS_BAD_PARAM;
+    if (cos_sin_cache == nullptr && !(base > 0.0f)) return TECOOPS_STATUS_BAD_PARAM;
+    if (!tecoops::is_16bit_float(dataType)) return TECOOPS_STATUS_BAD_PARAM;
+    const long long capacity = static_cast<long long>(num_blocks) * block_size;
+    if (capacity >= (1ll << 31)) return TECOOPS_STATUS_NOT_SUPPORTED;
+    FusedArgs a{};
+    a.positions = positions;
+    a.query = static_cast<uint16_t *>(query);
+    a.key = static_cast<uint16_t *>(key);
+    a.value = static_cast<const uint16_t *>(value);
+    a.slots = slot_mapping;
+    a.kcache = static_cast<uint16_t *>(key_cache);
+    a.vcache = static_cast<uint16_t *>(value_cache);
+    a.num_tokens = num_tokens;
+    a.num_heads = num_heads;
+    a.num_kv_heads = num_kv_heads;
+    a.head_size = head_size;
+    a.rot_dim = rot_dim;
+    a.q_stride = query_stride;
+    a.k_stride = key_stride;
+    a.v_stride = value_stride;
+    a.cos_sin_cache = cos_sin_cache;
+    a.max_position = max_position;
+    a.log2_base = cos_sin_cache ? 0.0f : log2f(base);
+    a.block_size = block_size;
+    a.lbs = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
+    a.capacity = capacity;
+    a.write_key = write_key;
+    // Vector path: 4 pairs per rotation task and 16-byte value / tail copies,
+    // all naturally aligned.
+    const int half = rot_dim / 2;
+    const size_t ra = is_neox ? 8 : 16;
+    bool vec = (half % 4) == 0 && (head_size % 8) == 0 && ((head_size - rot_dim) % 8) == 0 &&
+               (query_stride % 8) == 0 && (key_stride % 8) == 0 && (value_stride % 8) == 0 &&
+               tecoops::aligned(query, ra) && tecoops::aligned(key, ra) &&
+               tecoops::aligned(value, 16) && tecoops::aligned(key_cache, 16) &&
+               tecoops::aligned(value_cache, 16);
+    const unsigned grid = tecoops::ceil_div(num_tokens, kTokensPerBlock);
+    using tecoops::dev::bf16;
+    using tecoops::dev::f16;
+    hipStream_t s = handle->stream;
+    const bool h16 = dataType == TECOOPS_DATA_HALF;
+#define TECO_ROT_CACHE(TT, NX, VV) \
+    hipLaunchKernelGGL((rotary_cache_kernel<TT, NX, VV>), dim3(grid), dim3(kThreads), 0, s, a)
+    if (h16) {
+        if (is_neox) { if (vec) TECO_ROT_CACHE(f16, true, true); else TECO_ROT_CACHE(f16, true, false); }
+        else { if (vec) TECO_ROT_CACHE(f16, false, true); else TECO_ROT_CACHE(f16, false, false); }
+    } else {
+        if (is_neox) { if (vec) TECO_ROT_CACHE(bf16, true, true); else TECO_ROT_CACHE(bf16, true, false); }
+        else { if (vec) TECO_ROT_CACHE(bf16, false, true); else TECO_ROT_CACHE(bf16, false, false); }
+    }
+#undef TECO_ROT_CACHE
+    TECO_CHECK_LAUNCH("rotary_reshape_and_cache");
     return TECOOPS_STATUS_SUCCESS;
 }

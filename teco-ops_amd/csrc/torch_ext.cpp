@@ -182,6 +182,29 @@ void rotary_embedding(const Tensor &positions, Tensor &query, const c10::optiona
           "rotary_embedding");
 }
 
+void rotary_reshape_and_cache(const Tensor &positions, Tensor &query, Tensor &key,
+                              const Tensor &value, const Tensor &slot_mapping, Tensor &key_cache,
+                              Tensor &value_cache, int64_t head_size,
+                              const c10::optional<Tensor> &cos_sin_cache, bool is_neox,
+                              double base, int64_t rot_dim, bool write_key) {
+    need_cuda({&positions, &query, &key, &value, &slot_mapping, &key_cache, &value_cache});
+    const int64_t T = positions.numel();
+    const int H = query.numel() / (T * head_size);
+    const int Hkv = key.numel() / (T * head_size);
+    const int rd = rot_dim > 0 ? rot_dim
+                               : (cos_sin_cache.has_value() ? cos_sin_cache->size(1) : head_size);
+    check(tecoopsRotaryReshapeAndCache(
+              handle_for(query), positions.data_ptr<int64_t>(), query.data_ptr(), key.data_ptr(),
+              value.data_ptr(), slot_mapping.data_ptr<int64_t>(), key_cache.data_ptr(),
+              value_cache.data_ptr(), T, H, Hkv, head_size, rd, query.stride(0), key.stride(0),
+              value.stride(0),
+              cos_sin_cache.has_value() ? cos_sin_cache->data_ptr<float>() : nullptr,
+              cos_sin_cache.has_value() ? cos_sin_cache->size(0) : 0, static_cast<float>(base),
+              is_neox ? 1 : 0, key_cache.size(0), key_cache.size(2), write_key ? 1 : 0,
+              dtype_of(query)),
+          "rotary_reshape_and_cache");
+}
+
 void gemv(const Tensor &weight, const Tensor &x, Tensor &out) {
     need_cuda({&weight, &x, &out});
     const int B = x.dim() == 2 ? x.size(0) : 1;
@@ -223,6 +246,10 @@ TORCH_LIBRARY(tecoops, m) {
           "Tensor(b!)? conv_states, bool silu) -> ()");
     m.def("rotary_embedding(Tensor positions, Tensor(a!) query, Tensor(b!)? key, int head_size, "
           "Tensor? cos_sin_cache, bool is_neox, float base, int rot_dim) -> ()");
+    m.def("rotary_reshape_and_cache(Tensor positions, Tensor(a!) query, Tensor(b!) key, "
+          "Tensor value, Tensor slot_mapping, Tensor(c!) key_cache, Tensor(d!) value_cache, "
+          "int head_size, Tensor? cos_sin_cache, bool is_neox, float base, int rot_dim, "
+          "bool write_key) -> ()");
     m.def("gemv(Tensor weight, Tensor x, Tensor(a!) out) -> ()");
     m.def("gemv_int8(Tensor weight, Tensor scales, Tensor x, Tensor(a!) out) -> ()");
     m.def("memset(Tensor(a!) t, int value) -> ()");
@@ -235,6 +262,7 @@ TORCH_LIBRARY_IMPL(tecoops, CUDA, m) {
     m.impl("causal_conv1d_fn_torch", &causal_conv1d_fn_torch);
     m.impl("causal_conv1d", &causal_conv1d);
     m.impl("rotary_embedding", &rotary_embedding);
+    m.impl("rotary_reshape_and_cache", &rotary_reshape_and_cache);
     m.impl("gemv", &gemv);
     m.impl("gemv_int8", &gemv_int8);
     m.impl("memset", &memset_);

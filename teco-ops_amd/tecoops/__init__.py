@@ -39,7 +39,8 @@ __all__ = [
     "flatten_rays", "morton3D_invert", "reshape_and_cache", "rms_norm",
     "flash_attn_varlen_func", "causal_conv1d_fn_torch",
     # extensions
-    "rotary_embedding", "gemv", "gemv_int8", "causal_conv1d", "memset", "ops",
+    "rotary_embedding", "rotary_reshape_and_cache", "gemv", "gemv_int8", "causal_conv1d",
+    "memset", "ops",
 ]
 
 _handles = {}   # device index -> [handle, bound stream]
@@ -204,6 +205,30 @@ def rotary_embedding(positions, query, key, head_size, cos_sin_cache=None, is_ne
               key.stride(0) if key is not None else 0, _ptr(cos_sin_cache),
               cos_sin_cache.shape[0] if cos_sin_cache is not None else 0, float(base),
               int(bool(is_neox)), _dtype_code(query))
+
+
+def rotary_reshape_and_cache(positions, query, key, value, slot_mapping, key_cache, value_cache,
+                             head_size, cos_sin_cache=None, is_neox=True, base=10000.0,
+                             rot_dim=None, write_key=False):
+    """Decode step: rotary on query (in place) and key, then the rotated key and
+    value stored into the paged caches [num_blocks, Hkv, block_size, head_size]
+    at slot_mapping (int64); key is updated in place only when write_key."""
+    _check_cuda(positions, query, key, value, slot_mapping, key_cache, value_cache, cos_sin_cache)
+    if slot_mapping.dtype != torch.int64 or positions.dtype != torch.int64:
+        raise TypeError("positions and slot_mapping must be int64")
+    if cos_sin_cache is not None and cos_sin_cache.dtype != torch.float32:
+        raise TypeError("cos_sin_cache must be float32")
+    T = positions.numel()
+    H = query.numel() // (T * head_size)
+    Hkv = key.numel() // (T * head_size)
+    rd = rot_dim if rot_dim is not None else (
+        cos_sin_cache.shape[1] if cos_sin_cache is not None else head_size)
+    _lib.call("tecoopsRotaryReshapeAndCache", _handle(query.device), _ptr(positions), _ptr(query),
+              _ptr(key), _ptr(value), _ptr(slot_mapping), _ptr(key_cache), _ptr(value_cache),
+              T, H, Hkv, head_size, rd, query.stride(0), key.stride(0), value.stride(0),
+              _ptr(cos_sin_cache), cos_sin_cache.shape[0] if cos_sin_cache is not None else 0,
+              float(base), int(bool(is_neox)), key_cache.shape[0], key_cache.shape[2],
+              int(bool(write_key)), _dtype_code(query))
 
 
 def gemv(weight, x, out):

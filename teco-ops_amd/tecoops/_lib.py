@@ -68,6 +68,8 @@ SIGNATURES = {
     "tecoopsCausalConv1dEx": (I, [P, I, I, I, I, P, LL, LL, LL, P, LL, LL, LL, P, I, I, P, P, I,
                                   P, P, P, I, I, I]),
     "tecoopsRotaryEmbedding": (I, [P, P, P, P, I, I, I, I, I, LL, LL, P, I, F, I, I]),
+    "tecoopsRotaryReshapeAndCache": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, LL, LL, LL, P, I,
+                                         F, I, I, I, I, I]),
     "tecoopsGemv": (I, [P, P, P, P, I, I, I, I]),
     "tecoopsGemvInt8": (I, [P, P, P, P, P, I, I, I]),
 }

@@ -151,6 +151,82 @@ def test_rotary_partial_rot_dim_bf16_and_scalar_path():
     _run_rotary(64, 3, 1, 20, seed=7, rot_dim=10)   # rot/2 = 5: scalar path
 
 
+def _run_rotary_cache(T, H, Hkv, D, NB, BS, seed, is_neox=True, use_cache=False,
+                      dtype=orc.HALF, rot_dim=None, write_key=False, maxpos=2048):
+    """Fused decode step against (a) rotary_embedding then reshape_and_cache on
+    the GPU (bit-exact: same arithmetic) and (b) the oracle (q and cached k
+    within tolerance, cached v bit-exact)."""
+    r = rng(seed)
+    q = bits(r.standard_normal((T, H, D)), dtype)
+    k = bits(r.standard_normal((T, Hkv, D)), dtype)
+    v = bits(r.standard_normal((T, Hkv, D)), dtype)
+    pos = (np.arange(T) % maxpos).astype(np.int64)
+    r.shuffle(pos)
+    slots = r.permutation(NB * BS)[:T].astype(np.int64)
+    slots[::7] = -1                  # skipped
+    slots[3::11] = NB * BS + 5       # past the cache: skipped
+    rd = rot_dim or D
+    cache = None
+    if use_cache:
+        i = np.arange(rd // 2)
+        th = np.arange(maxpos)[:, None] * 10000.0 ** (-2 * i / rd)
+        cache = np.concatenate([np.cos(th), np.sin(th)], 1).astype(np.float32)
+    sentinel = bits(np.full((NB, Hkv, BS, D), 7.0), dtype)
+    # (a) two-kernel path on the GPU
+    q2, k2 = dev(q, dtype), dev(k, dtype)
+    kc2, vc2 = dev(sentinel, dtype), dev(sentinel, dtype)
+    tecoops.rotary_embedding(dev(pos), q2, k2, D, dev(cache) if use_cache else None,
+                             is_neox=is_neox, rot_dim=rd)
+    tecoops.reshape_and_cache(k2, dev(v, dtype), dev(slots), kc2, vc2)
+    # fused
+    q1, k1 = dev(q, dtype), dev(k, dtype)
+    kc1, vc1 = dev(sentinel, dtype), dev(sentinel, dtype)
+    tecoops.rotary_reshape_and_cache(dev(pos), q1, k1, dev(v, dtype), dev(slots), kc1, vc1, D,
+                                     dev(cache) if use_cache else None, is_neox=is_neox,
+                                     rot_dim=rd, write_key=write_key)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(q1), host_bits(q2)), "query differs from the two-kernel path"
+    assert np.array_equal(host_bits(kc1), host_bits(kc2)), "key cache differs"
+    assert np.array_equal(host_bits(vc1), host_bits(vc2)), "value cache differs"
+    if write_key:
+        assert np.array_equal(host_bits(k1), host_bits(k2)), "key differs"
+    else:
+        assert np.array_equal(host_bits(k1), k), "key changed without write_key"
+    # (b) oracle
+    qo, ko = orc.rotary_embedding(pos, q, k, rot_dim=rd, is_neox=is_neox, cos_sin_cache=cache,
+                                  dtype=dtype)
+    assert_close(as_f32(q1, dtype), qo, what="fused q")
+    kc_ref, vc_ref = sentinel.copy(), sentinel.copy()
+    orc.reshape_and_cache(np.zeros_like(k), v, slots, kc_ref, vc_ref)
+    assert np.array_equal(host_bits(vc1), vc_ref), "value cache vs oracle"
+    got_k = as_f32(kc1, dtype)
+    ok = (slots >= 0) & (slots < NB * BS)
+    for t in np.nonzero(ok)[0]:
+        blk, off = divmod(int(slots[t]), BS)
+        assert_close(got_k[blk, :, off, :], ko[t], what=f"cached k token {t}")
+    free = np.ones(NB * BS, bool)
+    free[slots[ok]] = False
+    untouched = got_k.transpose(0, 2, 1, 3).reshape(NB * BS, Hkv, D)[free]
+    assert (untouched == 7.0).all(), "slots outside slot_mapping were written"
+
+
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("use_cache", [False, True])
+def test_rotary_reshape_and_cache_variants(is_neox, use_cache):
+    _run_rotary_cache(300, 4, 2, 128, 40, 16, seed=21, is_neox=is_neox, use_cache=use_cache)
+
+
+def test_rotary_reshape_and_cache_partial_bf16_scalar_write_key():
+    _run_rotary_cache(64, 3, 1, 64, 12, 8, seed=22, rot_dim=32, dtype=orc.BF16, write_key=True)
+    _run_rotary_cache(50, 3, 2, 20, 10, 5, seed=23, rot_dim=10, write_key=True)  # scalar path
+
+
+def test_rotary_reshape_and_cache_baseline_shape():
+    """q [8192, 32, 128], k/v [8192, 8, 128] into 1024 blocks x 16 (the BASELINE
+    rotary and reshape_and_cache configs, as one decode-step op)."""
+    _run_rotary_cache(8192, 32, 8, 128, 1024, 16, seed=24)
+
+
 def test_rotary_baseline_config():
     """BASELINE config: q [8192, 32, 128], k [8192, 8, 128], positions 0..2047
     per sequence, base 10000, neox."""

@@ -34,7 +34,8 @@ def test_library_loaded_with_schemas():
     for name, schema in EXPECTED.items():
         op = getattr(torch.ops.tecoops, name).default
         assert str(op._schema) == "tecoops::" + schema
-    for name in ("causal_conv1d", "rotary_embedding", "gemv", "gemv_int8", "memset"):
+    for name in ("causal_conv1d", "rotary_embedding", "rotary_reshape_and_cache", "gemv",
+                 "gemv_int8", "memset"):
         assert hasattr(torch.ops.tecoops, name)
 
 
