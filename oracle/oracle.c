@@ -484,3 +484,84 @@ void orc_gemv_int8(const int8_t *weight, const uint16_t *scales, const uint16_t 
     }
     free(xf);
 }
+
+/* ------------------------------------------------- reference harness RNG
+ * libstdc++ semantics restated (pb_tools.h:123-200): minstd_rand0 seeded with
+ * s mod m (1 when that is 0); generate_canonical<double, 53> with
+ * R = max - min + 1 = 2^31 - 2 takes ceil(53 / floor(log2 R)) = 2 draws:
+ * (u1 - 1 + (u2 - 1) R) / R^2, clamped below 1; uniform = c (b - a) + a;
+ * normal = Marsaglia polar pairs (second value cached) scaled by sigma, plus mu.
+ * Pinned by the C++ standard's minstd_rand0 check value and by exact rational
+ * evaluation of the canonical formula in tests/test_harness_rng.py. */
+
+#define ORC_MINSTD_M 2147483647ull
+
+static uint64_t minstd_seed(long long s) {
+    /* result_type is unsigned long: a negative seed wraps before the modulo */
+    const uint64_t u = (uint64_t)s % ORC_MINSTD_M;
+    return u == 0 ? 1 : u;
+}
+
+static inline uint64_t minstd_next(uint64_t *x) {
+    *x = (*x * 16807ull) % ORC_MINSTD_M;
+    return *x;
+}
+
+static inline double canon53(uint64_t *x) {
+    const double r = 2147483646.0;
+    double sum = 0.0, tmp = 1.0;
+    for (int k = 0; k < 2; ++k) {
+        sum += (double)(minstd_next(x) - 1) * tmp;
+        tmp *= r;
+    }
+    double ret = sum / tmp;
+    if (ret >= 1.0) ret = nextafter(1.0, 0.0);
+    return ret;
+}
+
+uint32_t orc_minstd_nth(long long seed, size_t n) {
+    uint64_t x = minstd_seed(seed);
+    for (size_t i = 0; i < n; ++i) minstd_next(&x);
+    return (uint32_t)x;
+}
+
+void orc_harness_uniform(long long seed, size_t n, double lo, double hi, double *out) {
+    uint64_t x = minstd_seed(seed);
+    for (size_t i = 0; i < n; ++i) out[i] = canon53(&x) * (hi - lo) + lo;
+}
+
+void orc_harness_normal(long long seed, size_t n, double mu, double sigma, double *out) {
+    uint64_t x = minstd_seed(seed);
+    int saved_ok = 0;
+    double saved = 0.0;
+    for (size_t i = 0; i < n; ++i) {
+        double v;
+        if (saved_ok) {
+            saved_ok = 0;
+            v = saved;
+        } else {
+            double a, b, r2;
+            do {
+                a = 2.0 * canon53(&x) - 1.0;
+                b = 2.0 * canon53(&x) - 1.0;
+                r2 = a * a + b * b;
+            } while (r2 > 1.0 || r2 == 0.0);
+            const double mult = sqrt(-2 * log(r2) / r2);
+            saved = a * mult;
+            saved_ok = 1;
+            v = b * mult;
+        }
+        out[i] = v * sigma + mu;
+    }
+}
+
+void orc_harness_uniform_f32(long long seed, size_t n, float lo, float hi, float *out) {
+    uint64_t x = minstd_seed(seed);
+    /* generate_canonical<float, 24>: one draw; R rounds to 2^31 in float */
+    const float r = (float)2147483646.0;
+    for (size_t i = 0; i < n; ++i) {
+        float ret = (float)(minstd_next(&x) - 1) / r;
+        if (ret >= 1.0f) ret = nextafterf(1.0f, 0.0f);
+        out[i] = ret * (hi - lo) + lo;
+    }
+}

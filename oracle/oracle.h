@@ -85,6 +85,18 @@ void orc_gemv(const uint16_t *weight, const uint16_t *x, float *y,
 void orc_gemv_int8(const int8_t *weight, const uint16_t *scales, const uint16_t *x, float *y,
                    int batch, int n, int k);
 
+/* Input generation of the reference's C++ op tests
+ * (test/src/case/pb_tools.h:123-200, pb_tools.cpp:854-900): libstdc++'s
+ * std::default_random_engine (minstd_rand0: x <- 16807 x mod 2^31-1) driving
+ * uniform_real_distribution<double> and normal_distribution<double> (both
+ * through generate_canonical<double, 53>: two draws per canonical value) or,
+ * for bf16 tensors, uniform_real_distribution<float> (one draw).  One call
+ * is one serial chunk with its own seed. */
+uint32_t orc_minstd_nth(long long seed, size_t n);
+void orc_harness_uniform(long long seed, size_t n, double lo, double hi, double *out);
+void orc_harness_normal(long long seed, size_t n, double mu, double sigma, double *out);
+void orc_harness_uniform_f32(long long seed, size_t n, float lo, float hi, float *out);
+
 #ifdef __cplusplus
 }
 #endif
