@@ -64,20 +64,17 @@ def parse():
     return ap.parse_args()
 
 
-_GEN = None
-
-
 def seeded_bits(rng, shape, kind="normal", scale=1.0, lo=0.0, hi=1.0, dtype="f16"):
-    """Seeded synthetic tensor generated on the GPU (fp32, rounded to 16 bit)."""
+    """Seeded synthetic tensor generated on the GPU (fp32, rounded to 16 bit);
+    the torch generator is seeded from `rng`, so each op's data depends only
+    on its own seed."""
     import torch
-    global _GEN
-    if _GEN is None:
-        _GEN = torch.Generator(device="cuda")
-        _GEN.manual_seed(int(rng.integers(1 << 30)))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(int(rng.integers(1 << 30)))
     if kind == "normal":
-        t = torch.randn(shape, generator=_GEN, device="cuda") * scale
+        t = torch.randn(shape, generator=gen, device="cuda") * scale
     else:
-        t = torch.rand(shape, generator=_GEN, device="cuda") * (hi - lo) + lo
+        t = torch.rand(shape, generator=gen, device="cuda") * (hi - lo) + lo
     return t.to(torch.float16 if dtype == "f16" else torch.bfloat16)
 
 
@@ -96,7 +93,6 @@ def build_ops(names=None):
     import torch
     import tecoops
 
-    rng = np.random.default_rng(1000)
     ops = {}
 
     scale = 1.0 / math.sqrt(FA_D)
@@ -116,6 +112,7 @@ def build_ops(names=None):
         ops["copy_calibration"] = (fns, dict(bytes=2 * n))
 
     if want("rms_norm"):
+        rng = np.random.default_rng(1001)  # each op has its own seed
         # rms_norm [4096, 4096]
         ws = 2 * 4096 * 4096 * 2
         w = seeded_bits(rng, (4096,), "uniform", lo=0.5, hi=1.5)
@@ -127,6 +124,7 @@ def build_ops(names=None):
         ops["rms_norm"] = (fns, dict(bytes=2 * 4096 * 4096 * 2 + 4096 * 2))
 
     if want("reshape_and_cache"):
+        rng = np.random.default_rng(1002)  # each op has its own seed
         # reshape_and_cache: 8192 tokens into 1024 blocks x 16 slots
         T, Hkv, D, NB, BS = 8192, 8, 128, 1024, 16
         ws = 4 * T * Hkv * D * 2
@@ -142,6 +140,7 @@ def build_ops(names=None):
         ops["reshape_and_cache"] = (fns, dict(bytes=4 * T * Hkv * D * 2 + T * 8))
 
     if want("causal_conv1d"):
+        rng = np.random.default_rng(1003)  # each op has its own seed
         # causal_conv1d [8, 4096, 2048]
         B, C, L = 8, 4096, 2048
         ws = 2 * B * C * L * 2
@@ -157,6 +156,7 @@ def build_ops(names=None):
         ops["causal_conv1d"] = (fns, dict(bytes=2 * B * C * L * 2 + C * 4 * 2 + C * 2 + B * 3 * C * 2))
 
     if want("rotary"):
+        rng = np.random.default_rng(1004)  # each op has its own seed
         # rotary (in place)
         ws = 2 * (8192 * 40 * 128) * 2
         pos = torch.from_numpy((np.arange(8192) % 2048).astype(np.int64)).cuda()
@@ -168,6 +168,7 @@ def build_ops(names=None):
         ops["rotary"] = (fns, dict(bytes=2 * (8192 * 40 * 128) * 2 + 8192 * 8))
 
     if want("rotary_cache"):
+        rng = np.random.default_rng(1005)  # each op has its own seed
         # fused decode step: rotary on q (in place) and k, k and v into the
         # paged cache (rotary + reshape_and_cache configs as one pass)
         T, H, Hkv, D, NB, BS = 8192, 32, 8, 128, 1024, 16
@@ -186,6 +187,7 @@ def build_ops(names=None):
         ops["rotary_cache"] = (fns, dict(bytes=ws + 2 * T * 8))
 
     if want("gemv_f16_b1", "gemv_f16_b8", "gemv_i8_b1", "gemv_i8_b8"):
+        rng = np.random.default_rng(1006)  # each op has its own seed
         # GEMV: W fp16 / int8 [14336, 4096]
         N, K = 14336, 4096
         Ws = [seeded_bits(rng, (N, K), scale=0.02) for _ in range(copies_for(N * K * 2))]
@@ -202,6 +204,7 @@ def build_ops(names=None):
                                     dict(bytes=N * K + N * 2 + b * K * 2 + b * N * 2))
 
     if want("fa_prefill"):
+        rng = np.random.default_rng(1007)  # each op has its own seed
         # flash attention prefill: identity block tables over 4 x 256 blocks
         nbp = FA_S // 16
         fq = seeded_bits(rng, (FA_B * FA_S, FA_H, FA_D), dtype="bf16")
@@ -217,6 +220,7 @@ def build_ops(names=None):
             dict(flops=FA_PREFILL_FLOP, bytes=(fq.numel() * 2 + fk.numel() * 2) * 2))
 
     if want("fa_decode"):
+        rng = np.random.default_rng(1008)  # each op has its own seed
         # flash attention decode: B=64, seeded lengths U{512..8192}, shuffled blocks
         DB = 64
         lens = rng.integers(512, 8193, DB)
