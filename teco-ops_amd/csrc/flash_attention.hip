@@ -717,9 +717,17 @@ __global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
     }
 }
 
-// Merges the split partials of (b, kv head) into the output rows.
+// Merges the split partials of (b, kv head) into the output rows.  The
+// splits' (m, l) are staged in LDS once, one thread per column turns them into
+// normalised weights, and each output element then sums its splits' partial
+// O with independent loads.  Split counts beyond the LDS staging capacity
+// take a two-pass loop over global memory instead.
+constexpr int kCombineStage = 2048;  // (split, column) pairs staged in LDS
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256) fa_decode_combine_kernel(FaParams p) {
+    __shared__ float wgt[kCombineStage];  // [split][column]: m, then weight / total l
+    __shared__ float lsp[kCombineStage];  // [split][column]: l
     const int kvh = blockIdx.x % p.Hkv;
     const int b = blockIdx.x / p.Hkv;
     long long q_off;
@@ -730,17 +738,59 @@ __global__ void __launch_bounds__(256) fa_decode_combine_kernel(FaParams p) {
     int nsplit = S <= 0 ? 1 : (S + p.split_len - 1) / p.split_len;
     nsplit = min(nsplit, p.max_splits);
     const long long base = (static_cast<long long>(b) * p.Hkv + kvh) * p.max_splits;
-    for (int task = threadIdx.x; task < p.ncols * D; task += blockDim.x) {
+    const int nc = p.ncols;
+    if (nsplit * nc <= kCombineStage) {
+        // all (m, l) pairs in one round of parallel loads
+        for (int i = threadIdx.x; i < nsplit * nc; i += blockDim.x) {
+            const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + (base * nc + i) * 2);
+            wgt[i] = ml.x;
+            lsp[i] = ml.y;
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < nc; c += blockDim.x) {
+            float M = 0.0f;
+            for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, wgt[sp * nc + c]);
+            float l = 0.0f;
+            for (int sp = 0; sp < nsplit; ++sp) {
+                const float f = __builtin_amdgcn_exp2f(wgt[sp * nc + c] - M);
+                wgt[sp * nc + c] = f;
+                l += f * lsp[sp * nc + c];
+            }
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            for (int sp = 0; sp < nsplit; ++sp) wgt[sp * nc + c] *= inv;
+        }
+        __syncthreads();
+        for (int task = threadIdx.x; task < nc * D; task += blockDim.x) {
+            const int c = task / D, d = task % D;
+            const int hl = c / p.rq, row = c % p.rq;
+            if (hl >= p.G || row >= L) continue;
+            const float *src = p.ws_o + (base * nc + c) * D + d;
+            const long long step = static_cast<long long>(nc) * D;
+            float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+            int sp = 0;
+            for (; sp + 4 <= nsplit; sp += 4) {
+                acc0 += wgt[sp * nc + c] * src[sp * step];
+                acc1 += wgt[(sp + 1) * nc + c] * src[(sp + 1) * step];
+                acc2 += wgt[(sp + 2) * nc + c] * src[(sp + 2) * step];
+                acc3 += wgt[(sp + 3) * nc + c] * src[(sp + 3) * step];
+            }
+            for (; sp < nsplit; ++sp) acc0 += wgt[sp * nc + c] * src[sp * step];
+            const int h = kvh * p.G + hl;
+            p.o[((q_off + row) * p.H + h) * D + d] = Cvt<T>::from((acc0 + acc1) + (acc2 + acc3));
+        }
+        return;
+    }
+    for (int task = threadIdx.x; task < nc * D; task += blockDim.x) {
         const int c = task / D, d = task % D;
         const int hl = c / p.rq, row = c % p.rq;
         if (hl >= p.G || row >= L) continue;
         float M = 0.0f;
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.ws_ml[((base + s) * p.ncols + c) * 2]);
+        for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, p.ws_ml[((base + sp) * nc + c) * 2]);
         float acc = 0.0f, l = 0.0f;
-        for (int s = 0; s < nsplit; ++s) {
-            const float f = __builtin_amdgcn_exp2f(p.ws_ml[((base + s) * p.ncols + c) * 2] - M);
-            acc += f * p.ws_o[((base + s) * p.ncols + c) * D + d];
-            l += f * p.ws_ml[((base + s) * p.ncols + c) * 2 + 1];
+        for (int sp = 0; sp < nsplit; ++sp) {
+            const float f = __builtin_amdgcn_exp2f(p.ws_ml[((base + sp) * nc + c) * 2] - M);
+            acc += f * p.ws_o[((base + sp) * nc + c) * D + d];
+            l += f * p.ws_ml[((base + sp) * nc + c) * 2 + 1];
         }
         const float out = l > 0.0f ? acc / l : 0.0f;
         const int h = kvh * p.G + hl;

@@ -106,6 +106,17 @@ def test_decode_gqa_and_speculative_rows():
         check(case, orc.BF16, seed=H + ql)
 
 
+def test_decode_many_splits_combine_fallback():
+    """One sequence, 32 query heads on one kv head, 16K context: 128 splits x
+    32 columns exceed the combine kernel's LDS staging, so its two-pass path
+    runs; a second case with a few columns uses the staged path at the same
+    length."""
+    for H, Hkv in ((32, 1), (8, 2)):
+        case = dict(name=f"long{H}/{Hkv}", H=H, Hkv=Hkv, D=128, bs=16, q_lens=[1],
+                    kv_lens=[16384])
+        check(case, orc.BF16, seed=H)
+
+
 def test_softmax_scale_honoured():
     q, kc, vc, bt = make_inputs(6, 4, 2, 64, 16, [10], [30])
     got = run_gpu(q, kc, vc, bt, [10], [30], scale=0.3)
