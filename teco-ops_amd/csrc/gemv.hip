@@ -56,40 +56,60 @@ __device__ __forceinline__ void stage_x(uint4 *xs, const uint4 *x, int nvec) {
     __syncthreads();
 }
 
+// W chunks kept in flight per row ahead of their use; the first ones are
+// issued before x is staged in LDS, so the barrier that publishes x does not
+// delay the weight stream.  One chunk measured best (deeper rings were slower).
+constexpr int kPrefetch = 1;
+
 template <typename T, int B, int R>
 __global__ void __launch_bounds__(kThreads)
 gemv16_kernel(const uint4 *__restrict__ W, const uint4 *__restrict__ x, uint16_t *__restrict__ y,
               int N, int K) {
     extern __shared__ uint4 xs[];
     const int kv = K / 8;  // 16-byte chunks per row
-    stage_x(xs, x, B * kv);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n0 = (blockIdx.x * kWaves + wave) * R;
+    const uint4 *wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kv;
+    uint4 ring[kPrefetch][R];
+#pragma unroll
+    for (int i = 0; i < kPrefetch; ++i)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            ring[i][r] = lane + 64 * i < kv ? load_stream(wrow[r] + lane + 64 * i) : uint4{};
+    stage_x(xs, x, B * kv);
     if (n0 >= N) return;
     float acc[R][B];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
-    const uint4 *wrow[R];
+    for (int c0 = lane; c0 < kv; c0 += 64 * kPrefetch) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kv;
-#pragma unroll 2
-    for (int c = lane; c < kv; c += 64) {
-        uint4 wv[R];
+        for (int i = 0; i < kPrefetch; ++i) {
+            const int c = c0 + 64 * i;
+            if (c < kv) {
+                uint4 wv[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) wv[r] = load_stream(wrow[r] + c);
+                for (int r = 0; r < R; ++r) {
+                    wv[r] = ring[i][r];
+                    const int cn = c + 64 * kPrefetch;
+                    if (cn < kv) ring[i][r] = load_stream(wrow[r] + cn);
+                }
 #pragma unroll
-        for (int b = 0; b < B; ++b) {
-            const uint4 xv = xs[b * kv + c];
+                for (int b = 0; b < B; ++b) {
+                    const uint4 xv = xs[b * kv + c];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float s = acc[r][b];
-                s = Dot2<T>::run(wv[r].x, xv.x, s);
-                s = Dot2<T>::run(wv[r].y, xv.y, s);
-                s = Dot2<T>::run(wv[r].z, xv.z, s);
-                s = Dot2<T>::run(wv[r].w, xv.w, s);
-                acc[r][b] = s;
+                    for (int r = 0; r < R; ++r) {
+                        float s = acc[r][b];
+                        s = Dot2<T>::run(wv[r].x, xv.x, s);
+                        s = Dot2<T>::run(wv[r].y, xv.y, s);
+                        s = Dot2<T>::run(wv[r].z, xv.z, s);
+                        s = Dot2<T>::run(wv[r].w, xv.w, s);
+                        acc[r][b] = s;
+                    }
+                }
             }
         }
     }
@@ -120,40 +140,53 @@ gemv_i8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
     extern __shared__ uint4 xs[];
     const int kx = K / 8;    // 16-byte chunks of an x row (8 fp16)
     const int kw = K / 16;   // 16-byte chunks of a W row (16 int8)
-    stage_x(xs, x, B * kx);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n0 = (blockIdx.x * kWaves + wave) * R;
+    const uint4 *wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kw;
+    uint4 ring[kPrefetch][R];
+#pragma unroll
+    for (int i = 0; i < kPrefetch; ++i)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            ring[i][r] = lane + 64 * i < kw ? load_stream(wrow[r] + lane + 64 * i) : uint4{};
+    stage_x(xs, x, B * kx);
     if (n0 >= N) return;
     float acc[R][B];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
-    const uint4 *wrow[R];
+    for (int c0 = lane; c0 < kw; c0 += 64 * kPrefetch) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kw;
-#pragma unroll 2
-    for (int c = lane; c < kw; c += 64) {
-        uint32_t wh[R][8];  // 16 weights as 8 fp16 pairs
+        for (int i = 0; i < kPrefetch; ++i) {
+            const int c = c0 + 64 * i;
+            if (c < kw) {
+                uint32_t wh[R][8];  // 16 weights as 8 fp16 pairs
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint4 q = load_stream(wrow[r] + c);
-            widen_i8(q.x, wh[r][0], wh[r][1]);
-            widen_i8(q.y, wh[r][2], wh[r][3]);
-            widen_i8(q.z, wh[r][4], wh[r][5]);
-            widen_i8(q.w, wh[r][6], wh[r][7]);
-        }
+                for (int r = 0; r < R; ++r) {
+                    const uint4 q = ring[i][r];
+                    const int cn = c + 64 * kPrefetch;
+                    if (cn < kw) ring[i][r] = load_stream(wrow[r] + cn);
+                    widen_i8(q.x, wh[r][0], wh[r][1]);
+                    widen_i8(q.y, wh[r][2], wh[r][3]);
+                    widen_i8(q.z, wh[r][4], wh[r][5]);
+                    widen_i8(q.w, wh[r][6], wh[r][7]);
+                }
 #pragma unroll
-        for (int b = 0; b < B; ++b) {
-            const uint4 x0 = xs[b * kx + 2 * c];
-            const uint4 x1 = xs[b * kx + 2 * c + 1];
-            const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                for (int b = 0; b < B; ++b) {
+                    const uint4 x0 = xs[b * kx + 2 * c];
+                    const uint4 x1 = xs[b * kx + 2 * c + 1];
+                    const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float s = acc[r][b];
+                    for (int r = 0; r < R; ++r) {
+                        float s = acc[r][b];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) s = Dot2<f16>::run(wh[r][j], xv[j], s);
-                acc[r][b] = s;
+                        for (int j = 0; j < 8; ++j) s = Dot2<f16>::run(wh[r][j], xv[j], s);
+                        acc[r][b] = s;
+                    }
+                }
             }
         }
     }
