@@ -12,15 +12,17 @@
 // act is SiLU (v / (1 + exp(-v))); the reference always applies it.
 //
 // gfx950 design: every lane owns one channel d of one sequence and a chunk of
-// CH consecutive tokens; it loads its chunk plus the W-1 preceding inputs into
-// registers (a sliding window), so each input is fetched from HBM once and the
-// W-1 overlap comes from L1/L2.  Two lane mappings:
-//   SEQ_CONTIG (token stride 1, e.g. [batch, dim, seqlen]): consecutive lanes
-//     take consecutive chunks of one channel -> 16-byte loads/stores;
+// consecutive tokens held in registers with the W-1 inputs before it (a
+// sliding window), so each input is fetched from HBM once.  Two mappings:
+//   token stride 1 (e.g. [batch, dim, seqlen], the reference's [dim, tokens]):
+//     a wave streams whole rows, lanes on consecutive 8-token chunks ->
+//     16-byte loads / stores, the W-1 overlap passed between lanes in
+//     registers (conv1d_rows_kernel);
 //   otherwise (e.g. [tokens, dim]): consecutive lanes take consecutive
-//     channels of one chunk -> coalesced 2-byte accesses.
-// Only the chunk-0 lane of a (sequence, channel) touches conv_state, reading
-// the old state before writing the new one, so there is no cross-lane race.
+//     channels of one 16-token chunk -> coalesced 2-byte accesses, the overlap
+//     re-read through L1/L2 (conv1d_kernel).
+// Only one lane of a (sequence, channel) touches conv_state, reading the old
+// state before writing the new one, so there is no cross-lane race.
 // HBM-bound: algorithmic bytes = 2 * (x + out) + weights + bias + state.
 #include "common.h"
 #include "device.h"
@@ -148,111 +150,146 @@ __device__ __forceinline__ void conv1d_body(const ConvArgs &a, int b, int d, int
 }
 
 // Token-contiguous rows ([batch, dim, seqlen] and the reference's
-// [dim, tokens]): lane c of a (sequence, channel) row owns tokens
-// [8c, 8c + 8) and reads one 16-byte vector; the W-1 inputs before its chunk
-// are the last values of lane c-1's vector, taken with a lane shuffle (only the
-// first lane of each wave loads them).  grid = (chunk blocks, channels, batch).
+// [dim, tokens]): one wave streams whole (sequence, channel) rows.  The row is
+// cut into segments of 512 tokens, lane l owning tokens [8l, 8l + 8) of a
+// segment as one 16-byte vector; the loads of up to kSegs segments are issued
+// together, so every lane keeps kSegs vectors in flight.  The W-1 inputs
+// before a lane's tokens are the last values of lane l-1's vector (a lane
+// shuffle), of lane 63 of the previous segment (a readlane) for lane 0, and
+// the carried last values of the previous group of segments, or the prefix
+// (old conv state or zeros), at the start of a row.  A workgroup of 4 waves
+// takes 4 * kRowsPerWave consecutive rows.  Token stride is 1 (x and out).
+constexpr int kSegs = 4;
+constexpr int kRowsPerWave = 4;
+
 template <int W>
-__global__ void __launch_bounds__(256) conv1d_contig_kernel(ConvArgs a) {
-    constexpr int CH = 8;
-    const int b = blockIdx.z;
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {
+    constexpr int CH = 8, SEG = 64 * CH;
     const int lane = threadIdx.x & 63;
-    long long len, xoff, ooff;
-    if (a.qsl != nullptr) {
-        const long long s = a.qsl[b];
-        len = a.qsl[b + 1] - s;
-        xoff = s * a.xs;
-        ooff = s * a.os;
-    } else {
-        len = a.seq_len;
-        xoff = b * a.xb;
-        ooff = b * a.ob;
-    }
-    const int cidx = a.cidx ? a.cidx[b] : b;
-    if (cidx == a.pad_slot_id) return;  // uniform over the workgroup
-    if (static_cast<long long>(blockIdx.x) * blockDim.x * CH >= len) return;
-    const bool use_state =
-        a.state != nullptr && (a.api_mode == 1 || (a.hinit != nullptr && a.hinit[b] != 0));
-    for (int d = blockIdx.y; d < a.dim; d += gridDim.y) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const long long nrows = static_cast<long long>(a.batch) * a.dim;
+    const long long r0 = (static_cast<long long>(blockIdx.x) * 4 + wave) * kRowsPerWave;
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const long long r = r0 + rr;
+        if (r >= nrows) return;
+        const int b = static_cast<int>(r / a.dim), d = static_cast<int>(r % a.dim);
+        long long len, xoff, ooff;
+        if (a.qsl != nullptr) {
+            const long long s0 = a.qsl[b];
+            len = a.qsl[b + 1] - s0;
+            xoff = s0 * a.xs;
+            ooff = s0 * a.os;
+        } else {
+            len = a.seq_len;
+            xoff = b * a.xb;
+            ooff = b * a.ob;
+        }
+        const int cidx = a.cidx ? a.cidx[b] : b;
+        if (cidx == a.pad_slot_id || len <= 0) continue;
         const uint16_t *xr = a.x + xoff + d * a.xd;
         uint16_t *outr = a.out + ooff + d * a.od;
+        const bool use_state =
+            a.state != nullptr && (a.api_mode == 1 || (a.hinit != nullptr && a.hinit[b] != 0));
         uint16_t *st = a.state ? a.state + static_cast<long long>(cidx) * a.state_stride + d : nullptr;
-        const long long t0 = static_cast<long long>(c) * CH;
-        const bool full = t0 + CH <= len;
-        const bool vec = full && tecoops::aligned(xr + t0, 16);
-        float v[CH];
-        uint32_t dw[4];
-        if (vec) {
-            const uint4 q = *reinterpret_cast<const uint4 *>(xr + t0);
-            dw[0] = q.x; dw[1] = q.y; dw[2] = q.z; dw[3] = q.w;
-        } else {
-            uint16_t e[CH];
+        const bool vec_row = tecoops::aligned(xr, 16) && tecoops::aligned(outr, 16);
+        float wv[W];
 #pragma unroll
-            for (int j = 0; j < CH; ++j) e[j] = (t0 + j < len) ? xr[t0 + j] : 0;
+        for (int k = 0; k < W; ++k) wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
+        const float bv = a.bias ? h2f(a.bias[d]) : 0.0f;
+        // prefix[k]: full_x at position k - (W-1), the old state or zeros
+        uint16_t prefix[W - 1];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) dw[j] = e[2 * j] | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
-        }
+        for (int k = 0; k < W - 1; ++k) prefix[k] = use_state ? st[static_cast<long long>(k) * a.dim] : 0;
+        // carry[k]: full_x at position g0 - 3 + k for the current group start g0
+        float carry[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            v[2 * j] = lo<f16>(dw[j]);
-            v[2 * j + 1] = hi<f16>(dw[j]);
-        }
-        // last 4 values of the previous lane's chunk (all lanes take part)
-        const uint32_t p2 = __shfl_up(dw[2], 1, 64);
-        const uint32_t p3 = __shfl_up(dw[3], 1, 64);
-        float prev[3] = {hi<f16>(p2), lo<f16>(p3), hi<f16>(p3)};  // tokens t0-3, t0-2, t0-1
-        uint16_t prefix[3] = {0, 0, 0};
-        if (c == 0) {
+        for (int k = 0; k < W - 1; ++k) carry[3 - (W - 1) + k] = h2f(prefix[k]);
+
+        for (long long g0 = 0; g0 < len; g0 += kSegs * SEG) {
+            const int nseg = static_cast<int>(min<long long>(kSegs, (len - g0 + SEG - 1) / SEG));
+            uint32_t dw[kSegs][4];
 #pragma unroll
-            for (int k = 0; k < W - 1; ++k)
-                prefix[k] = use_state ? st[static_cast<long long>(k) * a.dim] : 0;
+            for (int u = 0; u < kSegs; ++u) {
+                if (u >= nseg) break;
+                const long long t0 = g0 + u * SEG + lane * CH;
+                if (vec_row && t0 + CH <= len) {
+                    const uint4 q = *reinterpret_cast<const uint4 *>(xr + t0);
+                    dw[u][0] = q.x; dw[u][1] = q.y; dw[u][2] = q.z; dw[u][3] = q.w;
+                } else {
+                    uint16_t e[CH];
 #pragma unroll
-            for (int k = 0; k < W - 1; ++k) prev[3 - (W - 1) + k] = h2f(prefix[k]);
-        } else if (lane == 0 && t0 < len) {
+                    for (int j = 0; j < CH; ++j) e[j] = (t0 + j < len) ? xr[t0 + j] : 0;
 #pragma unroll
-            for (int k = 0; k < 3; ++k) prev[k] = h2f(xr[t0 - 3 + k]);
-        }
-        if (t0 < len) {
-            float wv[W];
-#pragma unroll
-            for (int k = 0; k < W; ++k) wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
-            const float bv = a.bias ? h2f(a.bias[d]) : 0.0f;
-            float win[W - 1 + CH];
-#pragma unroll
-            for (int k = 0; k < W - 1; ++k) win[k] = prev[3 - (W - 1) + k];
-#pragma unroll
-            for (int j = 0; j < CH; ++j) win[W - 1 + j] = v[j];
-            float o[CH];
-#pragma unroll
-            for (int j = 0; j < CH; ++j) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < W; ++k) acc += win[j + k] * wv[k];
-                o[j] = act(acc + bv, a.silu);
-            }
-            if (vec && tecoops::aligned(outr + t0, 16)) {
-                uint4 q;
-                q.x = pack<f16>(o[0], o[1]);
-                q.y = pack<f16>(o[2], o[3]);
-                q.z = pack<f16>(o[4], o[5]);
-                q.w = pack<f16>(o[6], o[7]);
-                *reinterpret_cast<uint4 *>(outr + t0) = q;
-            } else {
-#pragma unroll
-                for (int j = 0; j < CH; ++j)
-                    if (t0 + j < len) outr[t0 + j] = f2h(o[j]);
-            }
-            if (c == 0 && st != nullptr) {
-                uint16_t ns[W - 1];
-#pragma unroll
-                for (int k = 0; k < W - 1; ++k) {
-                    const long long src = len - (W - 1) + k;
-                    ns[k] = src >= 0 ? xr[src] : prefix[W - 1 + src];
+                    for (int j = 0; j < 4; ++j)
+                        dw[u][j] = e[2 * j] | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
                 }
-#pragma unroll
-                for (int k = 0; k < W - 1; ++k) st[static_cast<long long>(k) * a.dim] = ns[k];
             }
+#pragma unroll
+            for (int u = 0; u < kSegs; ++u) {
+                if (u >= nseg) break;
+                const long long t0 = g0 + u * SEG + lane * CH;
+                // tokens t0-3 .. t0-1: lane-1's last three, or for lane 0 the
+                // previous segment's lane 63 (the carry for the first segment)
+                const uint32_t p2 = __shfl_up(dw[u][2], 1, 64);
+                const uint32_t p3 = __shfl_up(dw[u][3], 1, 64);
+                float prev[3] = {hi<f16>(p2), lo<f16>(p3), hi<f16>(p3)};
+                if (lane == 0) {
+                    if (u == 0) {
+                        prev[0] = carry[0]; prev[1] = carry[1]; prev[2] = carry[2];
+                    } else {
+                        const uint32_t q2 = __builtin_amdgcn_readlane(dw[u - 1][2], 63);
+                        const uint32_t q3 = __builtin_amdgcn_readlane(dw[u - 1][3], 63);
+                        prev[0] = hi<f16>(q2); prev[1] = lo<f16>(q3); prev[2] = hi<f16>(q3);
+                    }
+                }
+                float win[W - 1 + CH];
+#pragma unroll
+                for (int k = 0; k < W - 1; ++k) win[k] = prev[3 - (W - 1) + k];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    win[W - 1 + 2 * j] = lo<f16>(dw[u][j]);
+                    win[W - 1 + 2 * j + 1] = hi<f16>(dw[u][j]);
+                }
+                float o[CH];
+#pragma unroll
+                for (int j = 0; j < CH; ++j) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < W; ++k) acc += win[j + k] * wv[k];
+                    o[j] = act(acc + bv, a.silu);
+                }
+                if (vec_row && t0 + CH <= len) {
+                    uint4 q;
+                    q.x = pack<f16>(o[0], o[1]);
+                    q.y = pack<f16>(o[2], o[3]);
+                    q.z = pack<f16>(o[4], o[5]);
+                    q.w = pack<f16>(o[6], o[7]);
+                    *reinterpret_cast<uint4 *>(outr + t0) = q;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < CH; ++j)
+                        if (t0 + j < len) outr[t0 + j] = f2h(o[j]);
+                }
+            }
+            // the next group starts at g0 + kSegs * SEG only when this group was
+            // full, and then its last three tokens are lane 63's of segment kSegs-1
+            const uint32_t c2 = __builtin_amdgcn_readlane(dw[kSegs - 1][2], 63);
+            const uint32_t c3 = __builtin_amdgcn_readlane(dw[kSegs - 1][3], 63);
+            carry[0] = hi<f16>(c2); carry[1] = lo<f16>(c3); carry[2] = hi<f16>(c3);
+        }
+        if (lane == 0 && st != nullptr) {
+            uint16_t ns[W - 1];
+#pragma unroll
+            for (int k = 0; k < W - 1; ++k) {
+                const long long src = len - (W - 1) + k;
+                uint16_t old = 0;  // prefix[W - 1 + src] without a dynamic index
+#pragma unroll
+                for (int m = 0; m < W - 1; ++m)
+                    if (m == W - 1 + src) old = prefix[m];
+                ns[k] = src >= 0 ? xr[src] : old;
+            }
+#pragma unroll
+            for (int k = 0; k < W - 1; ++k) st[static_cast<long long>(k) * a.dim] = ns[k];
         }
     }
 }
@@ -275,10 +312,10 @@ template <int W>
 void launch(const ConvArgs &a0, bool seq_contig, long long max_len, hipStream_t s) {
     ConvArgs a = a0;
     if (seq_contig) {
-        constexpr int CH = 8;
-        a.nchunks = static_cast<int>((max_len + CH - 1) / CH);
-        dim3 grid(tecoops::ceil_div(a.nchunks, 256), a.dim < 65535 ? a.dim : 65535, a.batch);
-        hipLaunchKernelGGL((conv1d_contig_kernel<W>), grid, dim3(256), 0, s, a);
+        (void)max_len;
+        const long long rows = static_cast<long long>(a.batch) * a.dim;
+        const unsigned grid = static_cast<unsigned>(tecoops::ceil_div(rows, 4LL * kRowsPerWave));
+        hipLaunchKernelGGL((conv1d_rows_kernel<W>), dim3(grid), dim3(256), 0, s, a);
     } else {
         constexpr int CH = 16;
         a.nchunks = static_cast<int>((max_len + CH - 1) / CH);

@@ -204,14 +204,15 @@ gemv_i8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
 // ------------------------------------------------------------------ MFMA path
 //
 // Y^T = W X^T on v_mfma_f32_16x16x32_{f16,bf16}: A = 16 rows of W x 32 k,
-// B = X^T (32 k x 16 batch columns, columns >= B are zero).  Lane l supplies
-// A[row l%16][k 8*(l/16) .. +7] (one 16-byte load of W) and
+// B = X^T (32 k x 16 batch columns, of which the first B are stored).  Lane l
+// supplies A[row l%16][k 8*(l/16) .. +7] (one 16-byte load of W) and
 // B[k 8*(l/16) .. +7][column l%16] (one 16-byte load of x, L2-resident); it
 // receives C[row 4*(l/16) + v][column l%16], v < 4.  A workgroup owns RT*16
-// rows; its 4 waves take interleaved 32-k steps (split-K) and add their
-// partial C tiles through LDS.  For int8 weights a lane loads 16 weights
-// (16 bytes), widens them exactly to fp16 and feeds two MFMAs whose k order
-// is permuted consistently on A and B (k is a summation index).
+// rows; its 4 waves take interleaved 32-k steps (split-K), keep the W loads
+// of their next steps in flight in a register ring, and add their partial C
+// tiles through LDS.  For int8 weights a lane loads 16 weights (16 bytes),
+// widens them exactly to fp16 and feeds two MFMAs whose k order is permuted
+// consistently on A and B (k is a summation index).
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -237,21 +238,22 @@ __device__ __forceinline__ u32x4_t ld16_stream(const void *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
 }
 
-// Adds the 4 waves' partial tiles and writes y (scaled by s[n] when given).
-template <typename T, int RT>
+// Adds the NW waves' partial tiles and writes y (scaled by s[n] when given).
+template <typename T, int RT, int NW>
 __device__ __forceinline__ void gemv_mfma_epilogue(f32x4_t (&c)[RT], float *red, int n0, int N,
                                                    int B, uint16_t *y, const uint16_t *scales) {
+    static_assert(RT <= NW, "one wave finishes each row tile");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
-        *reinterpret_cast<f32x4_t *>(red + ((rt * 4 + wave) * 64 + lane) * 4) = c[rt];
+        *reinterpret_cast<f32x4_t *>(red + ((rt * NW + wave) * 64 + lane) * 4) = c[rt];
     __syncthreads();
-    // wave w finishes row tile w (RT <= 4)
+    // wave w finishes row tile w
     if (wave < RT) {
         f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w)
-            sum += *reinterpret_cast<const f32x4_t *>(red + ((wave * 4 + w) * 64 + lane) * 4);
+        for (int w = 0; w < NW; ++w)
+            sum += *reinterpret_cast<const f32x4_t *>(red + ((wave * NW + w) * 64 + lane) * 4);
         const int col = lane & 15;
         if (col < B) {
 #pragma unroll
@@ -266,35 +268,85 @@ __device__ __forceinline__ void gemv_mfma_epilogue(f32x4_t (&c)[RT], float *red,
     }
 }
 
-template <typename T, int RT>
-__global__ void __launch_bounds__(kThreads)
+// Runs one wave's n split-K steps (n wave-uniform) with the loads of each step
+// issued kRing steps ahead of its MFMAs: load(j, i) fetches step j into ring
+// slot i and use(i) consumes slot i.  Slot indices are compile-time constants
+// after unrolling, so the ring stays in registers and the waits before each
+// use leave the younger loads in flight.  Measured on the [14336, 4096]
+// batch-8 shapes, deeper rings do not pay: the fp16 kernel goes from 29 us at
+// depth 1 to 33 us at depth 4 (each load instruction already touches 16 rows
+// and the workgroups keep enough requests in flight), int8 with 4 row tiles
+// is flat (17.0 / 17.2 / 17.3 us at depths 1 / 2 / 4).
+constexpr int kRing = 1;
+
+template <int D, typename Load, typename Use>
+__device__ __forceinline__ void ring_steps(int n, Load &&load, Use &&use) {
+    if (n < D) {
+        for (int j = 0; j < n; ++j) {
+            load(j, 0);
+            use(0);
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < D; ++i) load(i, i);
+    int j = 0;
+    for (; j + 2 * D <= n; j += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            use(i);
+            load(j + D + i, i);
+            // keep this order: the scheduler would otherwise batch the loads
+            // at the end of the iteration and drain the ring at its top
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // steps j .. j+D-1 are in the ring; j+D .. n-1 (fewer than D) are not
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        use(i);
+        if (j + D + i < n) load(j + D + i, i);
+    }
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+        if (j + D + i < n) use(i);
+}
+
+// Wave w takes the 32-k (16-bit W) or 64-k (int8 W) steps w, w+4, w+8, ...
+// Columns >= B of the B operand read row B-1 of x: the C columns they produce
+// are never stored, and every value read is an element of x.
+template <typename T, int RT, int NW>
+__global__ void __launch_bounds__(NW * 64)
 gemv16_mfma_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x,
                    uint16_t *__restrict__ y, int N, int K, int B) {
-    __shared__ __attribute__((aligned(16))) float red[RT * kWaves * 64 * 4];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __attribute__((aligned(16))) float red[RT * NW * 64 * 4];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = blockIdx.x * (16 * RT);
     const int g = lane >> 4, col = lane & 15;
     const uint16_t *wr[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
-        wr[rt] = W + static_cast<long long>(min(n0 + rt * 16 + col, N - 1)) * K + 8 * g;
-    const bool xcol = col < B;
-    const uint16_t *xr = x + static_cast<long long>(min(col, B - 1)) * K + 8 * g;
+        wr[rt] = W + static_cast<long long>(min(n0 + rt * 16 + col, N - 1)) * K + 8 * g + 32 * wave;
+    const uint16_t *xr = x + static_cast<long long>(min(col, B - 1)) * K + 8 * g + 32 * wave;
     f32x4_t c[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) c[rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const int steps = K / 32;
-#pragma unroll 4
-    for (int st = wave; st < steps; st += kWaves) {
-        const int k0 = st * 32;
-        u32x4_t a[RT];
+    u32x4_t a[kRing][RT], b[kRing];
+    const int n = (K / 32 - wave + NW - 1) / NW;
+    ring_steps<kRing>(
+        n,
+        [&](int j, int i) {
+            const int k0 = j * (32 * NW);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) a[rt] = ld16_stream(wr[rt] + k0);
-        u32x4_t b = xcol ? ld16(xr + k0) : u32x4_t{0u, 0u, 0u, 0u};
+            for (int rt = 0; rt < RT; ++rt) a[i][rt] = ld16_stream(wr[rt] + k0);
+            b[i] = ld16(xr + k0);
+        },
+        [&](int i) {
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) c[rt] = Mma16<T>::run(a[rt], b, c[rt]);
-    }
-    gemv_mfma_epilogue<T, RT>(c, red, n0, N, B, y, nullptr);
+            for (int rt = 0; rt < RT; ++rt) c[rt] = Mma16<T>::run(a[i][rt], b[i], c[rt]);
+        });
+    gemv_mfma_epilogue<T, RT, NW>(c, red, n0, N, B, y, nullptr);
 }
 
 __device__ __forceinline__ void widen_i8x16(u32x4_t q, u32x4_t &lo8, u32x4_t &hi8) {
@@ -307,43 +359,45 @@ __device__ __forceinline__ void widen_i8x16(u32x4_t q, u32x4_t &lo8, u32x4_t &hi
     hi8 = u32x4_t{p[4], p[5], p[6], p[7]};
 }
 
-template <int RT>
-__global__ void __launch_bounds__(kThreads)
+template <int RT, int NW>
+__global__ void __launch_bounds__(NW * 64)
 gemv_i8_mfma_kernel(const int8_t *__restrict__ W, const uint16_t *__restrict__ scales,
                     const uint16_t *__restrict__ x, uint16_t *__restrict__ y, int N, int K,
                     int B) {
-    __shared__ __attribute__((aligned(16))) float red[RT * kWaves * 64 * 4];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __attribute__((aligned(16))) float red[RT * NW * 64 * 4];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = blockIdx.x * (16 * RT);
     const int g = lane >> 4, col = lane & 15;
     const int8_t *wr[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
-        wr[rt] = W + static_cast<long long>(min(n0 + rt * 16 + col, N - 1)) * K + 16 * g;
-    const bool xcol = col < B;
-    const uint16_t *xr = x + static_cast<long long>(min(col, B - 1)) * K + 16 * g;
+        wr[rt] = W + static_cast<long long>(min(n0 + rt * 16 + col, N - 1)) * K + 16 * g + 64 * wave;
+    const uint16_t *xr = x + static_cast<long long>(min(col, B - 1)) * K + 16 * g + 64 * wave;
     f32x4_t c[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) c[rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const int steps = K / 64;
-#pragma unroll 4
-    for (int st = wave; st < steps; st += kWaves) {
-        const int k0 = st * 64;
-        u32x4_t q[RT];
+    u32x4_t q[kRing][RT], b0[kRing], b1[kRing];
+    const int n = (K / 64 - wave + NW - 1) / NW;
+    ring_steps<kRing>(
+        n,
+        [&](int j, int i) {
+            const int k0 = j * (64 * NW);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) q[rt] = ld16_stream(wr[rt] + k0);
-        const u32x4_t zero = {0u, 0u, 0u, 0u};
-        const u32x4_t b0 = xcol ? ld16(xr + k0) : zero;
-        const u32x4_t b1 = xcol ? ld16(xr + k0 + 8) : zero;
+            for (int rt = 0; rt < RT; ++rt) q[i][rt] = ld16_stream(wr[rt] + k0);
+            b0[i] = ld16(xr + k0);
+            b1[i] = ld16(xr + k0 + 8);
+        },
+        [&](int i) {
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            u32x4_t a0, a1;
-            widen_i8x16(q[rt], a0, a1);
-            c[rt] = Mma16<f16>::run(a0, b0, c[rt]);
-            c[rt] = Mma16<f16>::run(a1, b1, c[rt]);
-        }
-    }
-    gemv_mfma_epilogue<f16, RT>(c, red, n0, N, B, y, scales);
+            for (int rt = 0; rt < RT; ++rt) {
+                u32x4_t a0, a1;
+                widen_i8x16(q[i][rt], a0, a1);
+                c[rt] = Mma16<f16>::run(a0, b0[i], c[rt]);
+                c[rt] = Mma16<f16>::run(a1, b1[i], c[rt]);
+            }
+        });
+    gemv_mfma_epilogue<f16, RT, NW>(c, red, n0, N, B, y, scales);
 }
 
 // Fallback for shapes the vector kernels do not take (K not a multiple of 8 /
@@ -371,6 +425,14 @@ gemv_scalar_kernel(const void *__restrict__ Wv, const uint16_t *__restrict__ sca
 }
 
 constexpr int kMaxLdsBytes = 64 * 1024;
+
+// Matrix-core path: smallest batch that takes it, row tiles of 16 per
+// workgroup and waves per workgroup.  int8 uses 4 row tiles per x fragment
+// (x is loaded as 32 bytes per 16 bytes of weights, so sharing it over more
+// rows pays: 19.9 -> 17.0 us at batch 8); for fp16 the extra tiles cost more
+// in parallelism than they save (28.7 us at 1 tile, 30.9 at 2).
+constexpr int kMfmaMinBatch16 = 3, kMfmaRT16 = 1, kMfmaWaves16 = 4;
+constexpr int kMfmaMinBatchI8 = 2, kMfmaRTI8 = 4, kMfmaWavesI8 = 8;
 
 template <typename T, int B>
 void launch16(const void *W, const void *x, void *y, int N, int K, hipStream_t s) {
@@ -431,19 +493,20 @@ extern "C" tecoopsStatus_t tecoopsGemv(tecoopsHandle_t handle, const void *weigh
     using tecoops::dev::bf16;
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
-    if (batch > 2 && (k % 32) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16)) {
-        constexpr int RT = 1;
+    if (batch >= kMfmaMinBatch16 && (k % 32) == 0 && tecoops::aligned(weight, 16) &&
+        tecoops::aligned(x, 16)) {
+        constexpr int RT = kMfmaRT16, NW = kMfmaWaves16;
         for (int b0 = 0; b0 < batch; b0 += 16) {
             const int nb = batch - b0 < 16 ? batch - b0 : 16;
             const uint16_t *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
             uint16_t *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
             const unsigned grid = tecoops::ceil_div(n, 16 * RT);
             if (dataType == TECOOPS_DATA_HALF)
-                hipLaunchKernelGGL((gemv16_mfma_kernel<f16, RT>), dim3(grid), dim3(kThreads), 0, s,
-                                   static_cast<const uint16_t *>(weight), xb, yb, n, k, nb);
-            else
-                hipLaunchKernelGGL((gemv16_mfma_kernel<bf16, RT>), dim3(grid), dim3(kThreads), 0,
+                hipLaunchKernelGGL((gemv16_mfma_kernel<f16, RT, NW>), dim3(grid), dim3(NW * 64), 0,
                                    s, static_cast<const uint16_t *>(weight), xb, yb, n, k, nb);
+            else
+                hipLaunchKernelGGL((gemv16_mfma_kernel<bf16, RT, NW>), dim3(grid), dim3(NW * 64),
+                                   0, s, static_cast<const uint16_t *>(weight), xb, yb, n, k, nb);
             TECO_CHECK_LAUNCH("gemv");
         }
         return TECOOPS_STATUS_SUCCESS;
@@ -484,14 +547,15 @@ extern "C" tecoopsStatus_t tecoopsGemvInt8(tecoopsHandle_t handle, const int8_t 
     if (batch <= 0 || n <= 0 || k <= 0) return TECOOPS_STATUS_BAD_PARAM;
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
-    if (batch > 1 && (k % 64) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16)) {
-        constexpr int RT = 1;
+    if (batch >= kMfmaMinBatchI8 && (k % 64) == 0 && tecoops::aligned(weight, 16) &&
+        tecoops::aligned(x, 16)) {
+        constexpr int RT = kMfmaRTI8, NW = kMfmaWavesI8;
         for (int b0 = 0; b0 < batch; b0 += 16) {
             const int nb = batch - b0 < 16 ? batch - b0 : 16;
             const uint16_t *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
             uint16_t *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
-            hipLaunchKernelGGL((gemv_i8_mfma_kernel<RT>), dim3(tecoops::ceil_div(n, 16 * RT)),
-                               dim3(kThreads), 0, s, weight, static_cast<const uint16_t *>(scales),
+            hipLaunchKernelGGL((gemv_i8_mfma_kernel<RT, NW>), dim3(tecoops::ceil_div(n, 16 * RT)),
+                               dim3(NW * 64), 0, s, weight, static_cast<const uint16_t *>(scales),
                                xb, yb, n, k, nb);
             TECO_CHECK_LAUNCH("gemv_int8");
         }

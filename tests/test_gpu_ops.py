@@ -302,6 +302,56 @@ def test_causal_conv1d_c_api_token_major():
         assert np.array_equal(host_bits(sd), st_ref)
 
 
+@pytest.mark.parametrize("W", [4, 3, 2])
+@pytest.mark.parametrize("L", [5000, 4999, 2051, 513])
+def test_causal_conv1d_long_rows(W, L):
+    """Token-contiguous rows longer than one group of loads (4 x 512 tokens),
+    so the last inputs of a group carry into the next; partial segments at
+    the end; L = 4999 / 2051 / 513 leave most rows misaligned for 16-byte
+    access; sequences 0 and 2 start from their conv state."""
+    r = rng(800 + 10 * W + L % 97)
+    B, dim = 3, 40
+    x = bits(r.standard_normal((B, dim, L)))
+    w = bits(r.normal(0, 0.5, (dim, W)))
+    bias = bits(r.standard_normal(dim))
+    st = bits(r.standard_normal((B, W - 1, dim)))
+    hinit = np.array([1, 0, 1], np.int8)
+    st_ref = st.copy()
+    ref = orc.causal_conv1d(x, w, bias=bias, conv_state=st_ref, has_initial_state=hinit,
+                            layout="bdl")
+    out = torch.empty((B, dim, L), dtype=torch.float16, device="cuda")
+    st_dev = dev(st)
+    tecoops.causal_conv1d(dev(x), dev(w), dev(bias), out, conv_states=st_dev,
+                          has_initial_state=dev(hinit))
+    torch.cuda.synchronize()
+    assert_close(as_f32(out), ref, what=f"conv W={W} L={L}")
+    assert np.array_equal(host_bits(st_dev), st_ref)
+
+
+def test_causal_conv1d_reference_layout_long_varlen():
+    """Reference torch layout [dim, tokens] with sequences of 3000, 7 and 2100
+    tokens (cache slots 2, 0, 1; slot 0 starts from zeros)."""
+    r = rng(900)
+    dim, lens = 24, [3000, 7, 2100]
+    total = sum(lens)
+    x = bits(r.standard_normal((dim, total)))
+    w = bits(r.standard_normal((4, dim)))
+    st = bits(r.standard_normal((3, 3, dim)))
+    qsl = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cidx = np.array([2, 0, 1], np.int32)
+    hinit = np.array([1, 0, 1], np.int8)
+    st_ref = st.copy()
+    ref = orc.causal_conv1d(x, w, conv_state=st_ref, query_start_loc=qsl, cache_indices=cidx,
+                            has_initial_state=hinit, layout="dl")
+    out = torch.zeros((dim, total), dtype=torch.float16, device="cuda")
+    st_dev = dev(st)
+    tecoops.causal_conv1d_fn_torch(out, st_dev, dev(x), dev(w), dev(qsl), dev(cidx), dev(hinit),
+                                   -1)
+    torch.cuda.synchronize()
+    assert_close(as_f32(out), ref, what="conv [dim, tokens] long varlen")
+    assert np.array_equal(host_bits(st_dev), st_ref)
+
+
 def test_causal_conv1d_baseline_config():
     """BASELINE config: x fp16 [8, 4096, 2048] ~N(0,1), weight [4096, 4]
     ~N(0,0.5), bias [4096] ~N(0,1), SiLU, final state written."""
@@ -350,6 +400,41 @@ def test_gemv_int8(B):
     # 1e-2 relative, with an absolute floor of 1e-3 of the output scale for
     # outputs that cancel to near zero
     assert_close(got, ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2, what=f"gemv_int8 B={B}")
+
+
+@pytest.mark.parametrize("K", [32, 224, 1248, 2080])
+@pytest.mark.parametrize("dt", [orc.HALF, orc.BF16])
+def test_gemv_matrix_core_ragged_k(K, dt):
+    """Batch 4 runs on the matrix-core path, whose 4 waves take the 32-k
+    steps w, w+4, ... of K: 1, 7, 39 and 65 steps give waves 0, 1, 2 and
+    several steps each, unequal step counts, and counts below, between and
+    above the multiples of the load-ahead depth."""
+    r = rng(600 + K)
+    N = 300
+    W = bits(r.normal(0, 0.05, (N, K)), dt)
+    x = bits(r.standard_normal((4, K)), dt)
+    ref = orc.gemv(W, x, dtype=dt)
+    y = torch.empty((4, N), dtype=torch.float16 if dt == orc.HALF else torch.bfloat16,
+                    device="cuda")
+    tecoops.gemv(dev(W, dt), dev(x, dt), y)
+    torch.cuda.synchronize()
+    assert_close(as_f32(y, dt), ref, what=f"gemv 4x{N}x{K}")
+
+
+@pytest.mark.parametrize("K", [64, 448, 1472, 4160])
+def test_gemv_int8_matrix_core_ragged_k(K):
+    """int8 steps are 64 k: 1, 7, 23 and 65 steps over 4 waves."""
+    r = rng(700 + K)
+    N = 200
+    W = r.integers(-127, 128, (N, K), dtype=np.int8)
+    s = bits(r.uniform(0.001, 0.01, N))
+    x = bits(r.standard_normal((3, K)))
+    ref = orc.gemv_int8(W, s, x)
+    y = torch.empty((3, N), dtype=torch.float16, device="cuda")
+    tecoops.gemv_int8(dev(W), dev(s), dev(x), y)
+    torch.cuda.synchronize()
+    assert_close(as_f32(y), ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2,
+                 what=f"gemv_int8 3x{N}x{K}")
 
 
 def test_gemv_odd_shapes_and_bf16():
