@@ -42,9 +42,16 @@ CFLAGS = [
 ]
 
 
+# Per-source flags.  Attention scores are never NaN for finite inputs (masked
+# scores are -inf), so the softmax max tree needs no NaN canonicalisation.
+EXTRA_FLAGS = {
+    "flash_attention.hip": ["-fno-honor-nans"],
+}
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd.insert(1, "-x")
         cmd.insert(2, "hip")

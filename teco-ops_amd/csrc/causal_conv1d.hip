@@ -213,7 +213,7 @@ __global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {
                 if (u >= nseg) break;
                 const long long t0 = g0 + u * SEG + lane * CH;
                 if (vec_row && t0 + CH <= len) {
-                    const uint4 q = *reinterpret_cast<const uint4 *>(xr + t0);
+                    const uint4 q = ld_stream(reinterpret_cast<const uint4 *>(xr + t0));
                     dw[u][0] = q.x; dw[u][1] = q.y; dw[u][2] = q.z; dw[u][3] = q.w;
                 } else {
                     uint16_t e[CH];
@@ -264,7 +264,7 @@ __global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {
                     q.y = pack<f16>(o[2], o[3]);
                     q.z = pack<f16>(o[4], o[5]);
                     q.w = pack<f16>(o[6], o[7]);
-                    *reinterpret_cast<uint4 *>(outr + t0) = q;
+                    st_stream(reinterpret_cast<uint4 *>(outr + t0), q);
                 } else {
 #pragma unroll
                     for (int j = 0; j < CH; ++j)

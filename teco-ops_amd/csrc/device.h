@@ -64,6 +64,25 @@ __device__ __forceinline__ uint32_t pack(float a, float b) {
     return static_cast<uint32_t>(Cvt<T>::from(a)) | (static_cast<uint32_t>(Cvt<T>::from(b)) << 16);
 }
 
+// Streaming 128-bit access for tensors touched once per launch: the
+// non-temporal policy keeps them from displacing reused data (weights, block
+// tables) in L2 / MALL.
+typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
+template <typename V>
+__device__ __forceinline__ V ld_stream(const V *p) {
+    if constexpr (sizeof(V) == 16)
+        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt *>(p)));
+    else
+        return __builtin_nontemporal_load(p);
+}
+template <typename V>
+__device__ __forceinline__ void st_stream(V *p, const V &v) {
+    if constexpr (sizeof(V) == 16)
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4_nt, v), reinterpret_cast<u32x4_nt *>(p));
+    else
+        __builtin_nontemporal_store(v, p);
+}
+
 // Value of lane l ^ 32 combined with lane l's own, through v_permlane32_swap
 // (a VALU lane-half swap on gfx950, no LDS round trip).  With both operands
 // equal to x, the swap returns {x[l], x[l + 32]} in lanes 0-31 and

@@ -14,27 +14,29 @@
 // on MI355X: one 16-byte vector per lane over a large grid).
 // HBM-bound: algorithmic bytes = 4 * num_tokens * H * D * 2 + 8 * num_tokens.
 #include "common.h"
+#include "device.h"
 
 namespace {
 
-// One lane per 16-byte chunk of one (token, head) row, key and value: the
-// grid is (ceil(per_token / 256), num_tokens) so no index division is needed
-// beyond one by vec_per_row.  Slot arithmetic is 32-bit (slots < 2^31 after
-// the range check), with a shift / mask when block_size is a power of two.
+// One lane per chunk (16 bytes when aligned) of one (token, head) row, key
+// and value, over a 1-D grid of num_tokens * per_token lanes (per launch
+// slice): every lane moves data whatever heads * head_size is.  Slot arithmetic
+// is 32-bit (slots < 2^31 after the range check), with a shift / mask when
+// block_size is a power of two.  Key and value are streamed (non-temporal).
 template <typename V, bool POW2>
 __global__ void __launch_bounds__(256)
 reshape_and_cache_kernel(const V *__restrict__ key, const V *__restrict__ value,
                          const int64_t *__restrict__ slot_mapping, V *__restrict__ key_cache,
                          V *__restrict__ value_cache, int heads, int vec_per_row, int block_size,
-                         int lbs, long long capacity) {
+                         int lbs, long long capacity, int total) {
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
     const int per_token = heads * vec_per_row;
-    const int rem = blockIdx.x * blockDim.x + threadIdx.x;
-    if (rem >= per_token) return;
-    const int t = blockIdx.y;
-    const long long src = static_cast<long long>(t) * per_token + rem;
+    const int t = gid / per_token;
+    const int rem = gid - t * per_token;
     const int64_t slot = slot_mapping[t];
-    const V kv = key[src];
-    const V vv = value[src];
+    const V kv = tecoops::dev::ld_stream(key + gid);
+    const V vv = tecoops::dev::ld_stream(value + gid);
     if (slot < 0 || slot >= capacity) return;
     const int s32 = static_cast<int>(slot);
     int blk, off;
@@ -49,8 +51,8 @@ reshape_and_cache_kernel(const V *__restrict__ key, const V *__restrict__ value,
     const int c = rem - h * vec_per_row;
     const long long dst =
         ((static_cast<long long>(blk) * heads + h) * block_size + off) * vec_per_row + c;
-    key_cache[dst] = kv;
-    value_cache[dst] = vv;
+    tecoops::dev::st_stream(key_cache + dst, kv);
+    tecoops::dev::st_stream(value_cache + dst, vv);
 }
 
 template <typename V>
@@ -60,20 +62,23 @@ tecoopsStatus_t launch(tecoopsHandle_t handle, const void *key, const void *valu
                        int block_size) {
     const long long per_token = static_cast<long long>(heads) * vec_per_row;
     const long long capacity = static_cast<long long>(num_blocks) * block_size;
-    if (capacity >= (1ll << 31) || per_token >= (1ll << 31)) {
+    if (capacity >= (1ll << 31) || per_token >= (1ll << 30)) {
         TECO_ERROR("reshape_and_cache: sizes beyond the supported index range");
         return TECOOPS_STATUS_NOT_SUPPORTED;
     }
     const int lbs = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
     auto *kern = lbs >= 0 ? &reshape_and_cache_kernel<V, true> : &reshape_and_cache_kernel<V, false>;
-    // grid.y is limited to 65535: longer token ranges run in slices
-    for (int t0 = 0; t0 < num_tokens; t0 += 65535) {
-        const int nt = num_tokens - t0 < 65535 ? num_tokens - t0 : 65535;
-        hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(per_token, 256), nt), dim3(256), 0,
-                           handle->stream, static_cast<const V *>(key) + t0 * per_token,
-                           static_cast<const V *>(value) + t0 * per_token, slot_mapping + t0,
-                           static_cast<V *>(key_cache), static_cast<V *>(value_cache), heads,
-                           vec_per_row, block_size, lbs, capacity);
+    // lane indices are 32-bit: tokens run in slices of fewer than 2^30 lanes
+    const int slice = static_cast<int>((1ll << 30) / per_token);
+    for (int t0 = 0; t0 < num_tokens; t0 += slice) {
+        const int nt = num_tokens - t0 < slice ? num_tokens - t0 : slice;
+        const int total = static_cast<int>(per_token * nt);
+        const long long src0 = static_cast<long long>(t0) * per_token;
+        hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(total, 256)), dim3(256), 0, handle->stream,
+                           static_cast<const V *>(key) + src0, static_cast<const V *>(value) + src0,
+                           slot_mapping + t0, static_cast<V *>(key_cache),
+                           static_cast<V *>(value_cache), heads, vec_per_row, block_size, lbs,
+                           capacity, total);
         TECO_CHECK_LAUNCH("reshape_and_cache");
     }
     return TECOOPS_STATUS_SUCCESS;

@@ -111,7 +111,7 @@ rms_norm_wave(const uint4 *__restrict__ x, const uint4 *__restrict__ w, const ui
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int c = lane + 64 * j;
-        if (c < vec_per_row) v[j] = xr[c];
+        if (c < vec_per_row) v[j] = ld_stream(xr + c);
     }
     float ss = 0.0f;
 #pragma unroll
@@ -120,7 +120,7 @@ rms_norm_wave(const uint4 *__restrict__ x, const uint4 *__restrict__ w, const ui
         if (c < vec_per_row) {
             uint32_t *pa = reinterpret_cast<uint32_t *>(&v[j]);
             if (ADD) {
-                const uint4 b = r[row * vec_per_row + c];
+                const uint4 b = ld_stream(r + row * vec_per_row + c);
                 const uint32_t *pb = reinterpret_cast<const uint32_t *>(&b);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -130,7 +130,7 @@ rms_norm_wave(const uint4 *__restrict__ x, const uint4 *__restrict__ w, const ui
                     ss += s1 * s1;
                     pa[q] = pack<T>(s0, s1);
                 }
-                r_out[row * vec_per_row + c] = v[j];
+                st_stream(r_out + row * vec_per_row + c, v[j]);
             } else {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -156,7 +156,7 @@ rms_norm_wave(const uint4 *__restrict__ x, const uint4 *__restrict__ w, const ui
             for (int q = 0; q < 4; ++q)
                 po[q] = pack<T>(lo<T>(pa[q]) * rstd * lo<T>(pw[q]),
                                 hi<T>(pa[q]) * rstd * hi<T>(pw[q]));
-            y[row * vec_per_row + c] = o;
+            st_stream(y + row * vec_per_row + c, o);
         }
     }
 }

@@ -8,9 +8,11 @@
 //
 // gfx950 design: one workgroup per 4 tokens.  The rot_dim/2 (cos, sin) pairs
 // of each token are computed once (accurate sincosf, or read from the cache)
-// into LDS and shared by all H + Hkv heads; each lane then rotates 4 pairs
-// per task with 8-byte (NeoX) or 16-byte (GPT-J) loads and stores.  HBM-bound: every byte
-// of q and k is read once and written once.
+// into LDS and shared by all H + Hkv heads; each lane then rotates 8 NeoX
+// pairs per task with two 16-byte loads and stores (4 pairs with 8-byte words
+// when only 8-byte alignment holds; 4 GPT-J pairs per 16-byte word), streamed
+// with the non-temporal policy.  HBM-bound: every byte of q and k is read
+// once and written once.
 #include "common.h"
 #include "device.h"
 
@@ -42,6 +44,17 @@ __device__ __forceinline__ void rot_neox4(const uint2 &a, const uint2 &b, const 
     ob = make_uint2(qb[0], qb[1]);
 }
 
+// Rotation of 8 NeoX pairs (x1 = a, x2 = b, 8 elements each, as 16-byte words).
+template <typename T>
+__device__ __forceinline__ void rot_neox8(const uint4 &a, const uint4 &b, const float2 *c,
+                                          uint4 &oa, uint4 &ob) {
+    uint2 lo_a, lo_b, hi_a, hi_b;
+    rot_neox4<T>(make_uint2(a.x, a.y), make_uint2(b.x, b.y), c, lo_a, lo_b);
+    rot_neox4<T>(make_uint2(a.z, a.w), make_uint2(b.z, b.w), c + 4, hi_a, hi_b);
+    oa = make_uint4(lo_a.x, lo_a.y, hi_a.x, hi_a.y);
+    ob = make_uint4(lo_b.x, lo_b.y, hi_b.x, hi_b.y);
+}
+
 // Rotation of 4 adjacent GPT-J pairs packed in 16 bytes.
 template <typename T>
 __device__ __forceinline__ uint4 rot_gptj4(const uint4 &a, const float2 *c) {
@@ -64,7 +77,9 @@ __device__ __forceinline__ void rot_pair(uint16_t x1b, uint16_t x2b, float2 cc, 
     o2 = Cvt<T>::from(x2 * cc.x + x1 * cc.y);
 }
 
-template <typename T, bool NEOX, bool VEC>
+// VW: 0 one pair per task; 1 four pairs (8-byte NeoX / 16-byte GPT-J words);
+// 2 eight NeoX pairs (16-byte words).  q and k are streamed (non-temporal).
+template <typename T, bool NEOX, int VW>
 __global__ void __launch_bounds__(kThreads)
 rotary_kernel(const int64_t *__restrict__ positions, uint16_t *__restrict__ query,
               uint16_t *__restrict__ key, int num_tokens, int num_heads, int num_kv_heads,
@@ -101,7 +116,7 @@ rotary_kernel(const int64_t *__restrict__ positions, uint16_t *__restrict__ quer
         skip[threadIdx.x] = sk;
     }
     __syncthreads();
-    constexpr int P = VEC ? 4 : 1;  // pairs per lane-task
+    constexpr int P = VW == 2 ? 8 : VW == 1 ? 4 : 1;  // pairs per lane-task
     const int tasks_per_head = half / P;
     const int heads = num_heads + (key ? num_kv_heads : 0);
     const int per_token = heads * tasks_per_head;
@@ -117,7 +132,14 @@ rotary_kernel(const int64_t *__restrict__ positions, uint16_t *__restrict__ quer
         const float2 *c = cs[tt];
         uint16_t *row = (is_q ? query + t * q_stride : key + t * k_stride) + h * head_size;
         if (NEOX) {
-            if (VEC) {
+            if (VW == 2) {
+                uint4 *p1 = reinterpret_cast<uint4 *>(row + i0);
+                uint4 *p2 = reinterpret_cast<uint4 *>(row + half + i0);
+                uint4 oa, ob;
+                rot_neox8<T>(ld_stream(p1), ld_stream(p2), c + i0, oa, ob);
+                st_stream(p1, oa);
+                st_stream(p2, ob);
+            } else if (VW == 1) {
                 uint2 *p1 = reinterpret_cast<uint2 *>(row + i0);
                 uint2 *p2 = reinterpret_cast<uint2 *>(row + half + i0);
                 uint2 oa, ob;
@@ -128,9 +150,9 @@ rotary_kernel(const int64_t *__restrict__ positions, uint16_t *__restrict__ quer
                 rot_pair<T>(row[i0], row[half + i0], c[i0], row[i0], row[half + i0]);
             }
         } else {
-            if (VEC) {
+            if (VW >= 1) {
                 uint4 *pp = reinterpret_cast<uint4 *>(row + 2 * i0);
-                *pp = rot_gptj4<T>(*pp, c + i0);
+                st_stream(pp, rot_gptj4<T>(ld_stream(pp), c + i0));
             } else {
                 rot_pair<T>(row[2 * i0], row[2 * i0 + 1], c[i0], row[2 * i0], row[2 * i0 + 1]);
             }
@@ -164,7 +186,7 @@ struct FusedArgs {
     int write_key;
 };
 
-template <typename T, bool NEOX, bool VEC>
+template <typename T, bool NEOX, int VW>
 __global__ void __launch_bounds__(kThreads) rotary_cache_kernel(FusedArgs a) {
     __shared__ float2 cs[kTokensPerBlock][kMaxHalf];
     __shared__ long long crow[kTokensPerBlock];  // first element of the token's cache row, or -1
@@ -203,8 +225,9 @@ __global__ void __launch_bounds__(kThreads) rotary_cache_kernel(FusedArgs a) {
         crow[threadIdx.x] = r;
     }
     __syncthreads();
-    constexpr int P = VEC ? 4 : 1;        // rotation pairs per task
-    constexpr int CV = VEC ? 8 : 1;       // elements per copy task
+    constexpr bool VEC = VW >= 1;
+    constexpr int P = VW == 2 ? 8 : VW == 1 ? 4 : 1;  // rotation pairs per task
+    constexpr int CV = VEC ? 8 : 1;                   // elements per copy task
     const int rot_tasks = half / P;       // per head
     const int tail = D - a.rot_dim;       // key elements past rot_dim: copied unrotated
     const int tail_tasks = (tail + CV - 1) / CV;
@@ -225,7 +248,14 @@ __global__ void __launch_bounds__(kThreads) rotary_cache_kernel(FusedArgs a) {
             const int i0 = (local - h * rot_tasks) * P;
             uint16_t *row = a.query + t * a.q_stride + h * D;
             if (NEOX) {
-                if (VEC) {
+                if (VW == 2) {
+                    uint4 *p1 = reinterpret_cast<uint4 *>(row + i0);
+                    uint4 *p2 = reinterpret_cast<uint4 *>(row + half + i0);
+                    uint4 oa, ob;
+                    rot_neox8<T>(ld_stream(p1), ld_stream(p2), c + i0, oa, ob);
+                    st_stream(p1, oa);
+                    st_stream(p2, ob);
+                } else if (VEC) {
                     uint2 *p1 = reinterpret_cast<uint2 *>(row + i0);
                     uint2 *p2 = reinterpret_cast<uint2 *>(row + half + i0);
                     uint2 oa, ob;
@@ -238,7 +268,7 @@ __global__ void __launch_bounds__(kThreads) rotary_cache_kernel(FusedArgs a) {
             } else {
                 if (VEC) {
                     uint4 *pp = reinterpret_cast<uint4 *>(row + 2 * i0);
-                    *pp = rot_gptj4<T>(*pp, c + i0);
+                    st_stream(pp, rot_gptj4<T>(ld_stream(pp), c + i0));
                 } else {
                     rot_pair<T>(row[2 * i0], row[2 * i0 + 1], c[i0], row[2 * i0], row[2 * i0 + 1]);
                 }
@@ -260,7 +290,20 @@ __global__ void __launch_bounds__(kThreads) rotary_cache_kernel(FusedArgs a) {
             }
             const int i0 = r * P;
             if (NEOX) {
-                if (VEC) {
+                if (VW == 2) {
+                    uint4 oa, ob;
+                    rot_neox8<T>(ld_stream(reinterpret_cast<const uint4 *>(row + i0)),
+                                 ld_stream(reinterpret_cast<const uint4 *>(row + half + i0)), c + i0,
+                                 oa, ob);
+                    if (a.write_key) {
+                        st_stream(reinterpret_cast<uint4 *>(row + i0), oa);
+                        st_stream(reinterpret_cast<uint4 *>(row + half + i0), ob);
+                    }
+                    if (dst != nullptr) {
+                        st_stream(reinterpret_cast<uint4 *>(dst + i0), oa);
+                        st_stream(reinterpret_cast<uint4 *>(dst + half + i0), ob);
+                    }
+                } else if (VEC) {
                     uint2 oa, ob;
                     rot_neox4<T>(*reinterpret_cast<const uint2 *>(row + i0),
                                  *reinterpret_cast<const uint2 *>(row + half + i0), c + i0, oa, ob);
@@ -286,9 +329,9 @@ __global__ void __launch_bounds__(kThreads) rotary_cache_kernel(FusedArgs a) {
                 }
             } else {
                 if (VEC) {
-                    const uint4 o = rot_gptj4<T>(*reinterpret_cast<const uint4 *>(row + 2 * i0), c + i0);
-                    if (a.write_key) *reinterpret_cast<uint4 *>(row + 2 * i0) = o;
-                    if (dst != nullptr) *reinterpret_cast<uint4 *>(dst + 2 * i0) = o;
+                    const uint4 o = rot_gptj4<T>(ld_stream(reinterpret_cast<const uint4 *>(row + 2 * i0)), c + i0);
+                    if (a.write_key) st_stream(reinterpret_cast<uint4 *>(row + 2 * i0), o);
+                    if (dst != nullptr) st_stream(reinterpret_cast<uint4 *>(dst + 2 * i0), o);
                 } else {
                     uint16_t o1, o2;
                     rot_pair<T>(row[2 * i0], row[2 * i0 + 1], c[i0], o1, o2);
@@ -311,25 +354,31 @@ __global__ void __launch_bounds__(kThreads) rotary_cache_kernel(FusedArgs a) {
         const uint16_t *src = a.value + t * a.v_stride + h * D + e0;
         uint16_t *dst = a.vcache + cr + h * head_stride + e0;
         if (VEC)
-            *reinterpret_cast<uint4 *>(dst) = *reinterpret_cast<const uint4 *>(src);
+            st_stream(reinterpret_cast<uint4 *>(dst), ld_stream(reinterpret_cast<const uint4 *>(src)));
         else
             *dst = *src;
     }
 }
 
+template <typename T, bool NEOX, int VW>
+void launch_vw(int T_, hipStream_t s, const int64_t *pos, void *q, void *k, int H, int Hkv, int D,
+               int rot, long long qs, long long ks, const float *cache, int maxpos, float lb) {
+    const unsigned grid = tecoops::ceil_div(T_, kTokensPerBlock);
+    hipLaunchKernelGGL((rotary_kernel<T, NEOX, VW>), dim3(grid), dim3(kThreads), 0, s, pos,
+                       static_cast<uint16_t *>(q), static_cast<uint16_t *>(k), T_, H, Hkv, D, rot,
+                       qs, ks, cache, maxpos, lb);
+}
+
 template <typename T, bool NEOX>
-void launch(bool vec, int T_, hipStream_t s, const int64_t *pos, void *q, void *k, int H,
+void launch(int vw, int T_, hipStream_t s, const int64_t *pos, void *q, void *k, int H,
             int Hkv, int D, int rot, long long qs, long long ks, const float *cache, int maxpos,
             float lb) {
-    const unsigned grid = tecoops::ceil_div(T_, kTokensPerBlock);
-    if (vec)
-        hipLaunchKernelGGL((rotary_kernel<T, NEOX, true>), dim3(grid), dim3(kThreads), 0, s, pos,
-                           static_cast<uint16_t *>(q), static_cast<uint16_t *>(k), T_, H, Hkv, D,
-                           rot, qs, ks, cache, maxpos, lb);
+    if (vw == 2)
+        launch_vw<T, NEOX, NEOX ? 2 : 1>(T_, s, pos, q, k, H, Hkv, D, rot, qs, ks, cache, maxpos, lb);
+    else if (vw == 1)
+        launch_vw<T, NEOX, 1>(T_, s, pos, q, k, H, Hkv, D, rot, qs, ks, cache, maxpos, lb);
     else
-        hipLaunchKernelGGL((rotary_kernel<T, NEOX, false>), dim3(grid), dim3(kThreads), 0, s, pos,
-                           static_cast<uint16_t *>(q), static_cast<uint16_t *>(k), T_, H, Hkv, D,
-                           rot, qs, ks, cache, maxpos, lb);
+        launch_vw<T, NEOX, 0>(T_, s, pos, q, k, H, Hkv, D, rot, qs, ks, cache, maxpos, lb);
 }
 
 }  // namespace
@@ -355,30 +404,36 @@ extern "C" tecoopsStatus_t tecoopsRotaryEmbedding(tecoopsHandle_t handle,
     if (cos_sin_cache == nullptr && !(base > 0.0f)) return TECOOPS_STATUS_BAD_PARAM;
     if (!tecoops::is_16bit_float(dataType)) return TECOOPS_STATUS_BAD_PARAM;
     const int half = rot_dim / 2;
-    // Vector path: 4 pairs per lane with naturally aligned 8 / 16 byte accesses.
+    // Vector paths: 4 pairs per lane with naturally aligned 8 / 16 byte
+    // accesses, or 8 NeoX pairs per lane in 16-byte words.
     const size_t align = is_neox ? 8 : 16;
     bool vec = (half % 4) == 0 && (head_size % 4) == 0 && (query_stride % 4) == 0 &&
                tecoops::aligned(query, align);
     if (key != nullptr) vec = vec && (key_stride % 4) == 0 && tecoops::aligned(key, align);
     if (!is_neox) vec = vec && (head_size % 8) == 0 && (query_stride % 8) == 0 &&
                         (key == nullptr || (key_stride % 8) == 0);
+    // NeoX with 8 pairs per lane: both halves in 16-byte words
+    bool wide = is_neox && vec && (half % 8) == 0 && (head_size % 8) == 0 &&
+                (query_stride % 8) == 0 && tecoops::aligned(query, 16);
+    if (key != nullptr) wide = wide && (key_stride % 8) == 0 && tecoops::aligned(key, 16);
+    const int vw = wide ? 2 : vec ? 1 : 0;
     const float lb = cos_sin_cache ? 0.0f : log2f(base);
     const int Hkv = key ? num_kv_heads : 0;
     using tecoops::dev::bf16;
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
     if (dataType == TECOOPS_DATA_HALF) {
-        if (is_neox) launch<f16, true>(vec, num_tokens, s, positions, query, key, num_heads, Hkv,
+        if (is_neox) launch<f16, true>(vw, num_tokens, s, positions, query, key, num_heads, Hkv,
                                        head_size, rot_dim, query_stride, key_stride,
                                        cos_sin_cache, max_position, lb);
-        else launch<f16, false>(vec, num_tokens, s, positions, query, key, num_heads, Hkv,
+        else launch<f16, false>(vw, num_tokens, s, positions, query, key, num_heads, Hkv,
                                 head_size, rot_dim, query_stride, key_stride, cos_sin_cache,
                                 max_position, lb);
     } else {
-        if (is_neox) launch<bf16, true>(vec, num_tokens, s, positions, query, key, num_heads, Hkv,
+        if (is_neox) launch<bf16, true>(vw, num_tokens, s, positions, query, key, num_heads, Hkv,
                                         head_size, rot_dim, query_stride, key_stride,
                                         cos_sin_cache, max_position, lb);
-        else launch<bf16, false>(vec, num_tokens, s, positions, query, key, num_heads, Hkv,
+        else launch<bf16, false>(vw, num_tokens, s, positions, query, key, num_heads, Hkv,
                                  head_size, rot_dim, query_stride, key_stride, cos_sin_cache,
                                  max_position, lb);
     }
@@ -434,8 +489,8 @@ extern "C" tecoopsStatus_t tecoopsRotaryReshapeAndCache(
     a.lbs = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
     a.capacity = capacity;
     a.write_key = write_key;
-    // Vector path: 4 pairs per rotation task and 16-byte value / tail copies,
-    // all naturally aligned.
+    // Vector path: 4 (or 8) pairs per rotation task and 16-byte value / tail
+    // copies, all naturally aligned.
     const int half = rot_dim / 2;
     const size_t ra = is_neox ? 8 : 16;
     bool vec = (half % 4) == 0 && (head_size % 8) == 0 && ((head_size - rot_dim) % 8) == 0 &&
@@ -443,6 +498,9 @@ extern "C" tecoopsStatus_t tecoopsRotaryReshapeAndCache(
                tecoops::aligned(query, ra) && tecoops::aligned(key, ra) &&
                tecoops::aligned(value, 16) && tecoops::aligned(key_cache, 16) &&
                tecoops::aligned(value_cache, 16);
+    // NeoX with 8 pairs per lane: both halves in 16-byte words
+    const bool wide = is_neox && vec && (half % 8) == 0 && tecoops::aligned(query, 16) &&
+                      tecoops::aligned(key, 16);
     const unsigned grid = tecoops::ceil_div(num_tokens, kTokensPerBlock);
     using tecoops::dev::bf16;
     using tecoops::dev::f16;
@@ -451,11 +509,21 @@ extern "C" tecoopsStatus_t tecoopsRotaryReshapeAndCache(
 #define TECO_ROT_CACHE(TT, NX, VV) \
     hipLaunchKernelGGL((rotary_cache_kernel<TT, NX, VV>), dim3(grid), dim3(kThreads), 0, s, a)
     if (h16) {
-        if (is_neox) { if (vec) TECO_ROT_CACHE(f16, true, true); else TECO_ROT_CACHE(f16, true, false); }
-        else { if (vec) TECO_ROT_CACHE(f16, false, true); else TECO_ROT_CACHE(f16, false, false); }
+        if (is_neox) {
+            if (wide) TECO_ROT_CACHE(f16, true, 2);
+            else if (vec) TECO_ROT_CACHE(f16, true, 1);
+            else TECO_ROT_CACHE(f16, true, 0);
+        } else {
+            if (vec) TECO_ROT_CACHE(f16, false, 1); else TECO_ROT_CACHE(f16, false, 0);
+        }
     } else {
-        if (is_neox) { if (vec) TECO_ROT_CACHE(bf16, true, true); else TECO_ROT_CACHE(bf16, true, false); }
-        else { if (vec) TECO_ROT_CACHE(bf16, false, true); else TECO_ROT_CACHE(bf16, false, false); }
+        if (is_neox) {
+            if (wide) TECO_ROT_CACHE(bf16, true, 2);
+            else if (vec) TECO_ROT_CACHE(bf16, true, 1);
+            else TECO_ROT_CACHE(bf16, true, 0);
+        } else {
+            if (vec) TECO_ROT_CACHE(bf16, false, 1); else TECO_ROT_CACHE(bf16, false, 0);
+        }
     }
 #undef TECO_ROT_CACHE
     TECO_CHECK_LAUNCH("rotary_reshape_and_cache");
