@@ -122,6 +122,15 @@ __device__ __forceinline__ void seq_info(const FaParams &p, int b, long long &q_
     }
 }
 
+// 16-byte K/V load; STREAM selects the non-temporal policy for data read once.
+template <bool STREAM>
+__device__ __forceinline__ u32x4 load16(const uint16_t *p) {
+    if constexpr (STREAM)
+        return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    else
+        return *reinterpret_cast<const u32x4 *>(p);
+}
+
 // Element offset of key row `kv` of the (sequence, kv head) whose block-table
 // row is bt_row and whose head offset inside a block is head_off.  Rows at or
 // beyond kv_limit, and rows whose page id is out of range, are redirected to
@@ -151,7 +160,7 @@ __device__ __forceinline__ long long row_offset(const FaParams &p, const int *bt
 // threads.  K is stored row-major [TILE][D + 8]; V transposed [D][TILE + 4].
 // Each thread owns one 16-byte column of K (rows r0, r0 + KRS, ...) and
 // VPT (4-row x 8-column) blocks of V.
-template <int D, int TILE, int NT, bool POW2>
+template <int D, int TILE, int NT, bool POW2, bool STREAM = false>
 struct TileLoader {
     static constexpr int KP = D + 8;
     static constexpr int VP = TILE + 4;
@@ -177,7 +186,7 @@ struct TileLoader {
             bool ok;
             const long long o = row_offset<D, POW2>(p, bt_row, head_off, j0 + r0 + i * KRS,
                                                     kv_limit, ok);
-            k[i] = *reinterpret_cast<const u32x4 *>(p.kc + o + col * 8);
+            k[i] = load16<STREAM>(p.kc + o + col * 8);
         }
         // Invalid V rows are zeroed in store(), so the wave does not wait for
         // the loads here.
@@ -192,7 +201,7 @@ struct TileLoader {
                 bool ok;
                 const long long o = row_offset<D, POW2>(p, bt_row, head_off, j0 + 4 * rg + r,
                                                         kv_limit, ok);
-                v[i][r] = *reinterpret_cast<const u32x4 *>(p.vc + o + cg * 8);
+                v[i][r] = load16<STREAM>(p.vc + o + cg * 8);
                 vok |= (ok ? 1u : 0u) << (4 * i + r);
             }
         }
@@ -240,7 +249,7 @@ struct TileLoader {
 // global loads never wait for it.  Same LDS layout as TileLoader: K [TILE][D +
 // 8], V^T [D][TILE + 4].  load() must be called for consecutive tiles after
 // one prefetch() of the first.
-template <int TILE, int W>
+template <int TILE, int W, bool STREAM = false>
 struct PagedLoader128 {
     static constexpr int D = 128;
     static constexpr int KP = D + 8;
@@ -292,7 +301,7 @@ struct PagedLoader128 {
         for (int i = 0; i < KI; ++i) {
             const int row0 = j0 + w * RW + 4 * i;
             const long long base = group_base(p, head_off, row0, pg[i]);
-            k[i] = *reinterpret_cast<const u32x4 *>(p.kc + base + kr * D + kc * 8);
+            k[i] = load16<STREAM>(p.kc + base + kr * D + kc * 8);
         }
         // V rows at or past kv_limit are zeroed in store(), not here: a select
         // on the loaded value would make the wave wait for the load at once.
@@ -302,8 +311,8 @@ struct PagedLoader128 {
             const int row0 = j0 + w * RW + 8 * i;
             const long long base = group_base(p, head_off, row0, pg[KI + i]);
             const uint16_t *src = p.vc + base + vr * D + vc * 8;
-            v[i][0] = *reinterpret_cast<const u32x4 *>(src);
-            v[i][1] = *reinterpret_cast<const u32x4 *>(src + D);
+            v[i][0] = load16<STREAM>(src);
+            v[i][1] = load16<STREAM>(src + D);
             vok |= (row0 + vr < kv_limit ? 1u : 0u) << (2 * i);
             vok |= (row0 + vr + 1 < kv_limit ? 1u : 0u) << (2 * i + 1);
         }
@@ -339,13 +348,14 @@ struct PagedLoader128 {
 };
 
 // Loader choice: the uniform-page loader when it applies, else TileLoader.
-template <int D, int TILE, int W, bool POW2>
+// STREAM marks K/V read once per launch (decode): non-temporal loads.
+template <int D, int TILE, int W, bool POW2, bool STREAM = false>
 struct LoaderSel {
-    using type = TileLoader<D, TILE, W * 64, POW2>;
+    using type = TileLoader<D, TILE, W * 64, POW2, STREAM>;
 };
-template <int TILE, int W>
-struct LoaderSel<128, TILE, W, true> {
-    using type = PagedLoader128<TILE, W>;
+template <int TILE, int W, bool STREAM>
+struct LoaderSel<128, TILE, W, true, STREAM> {
+    using type = PagedLoader128<TILE, W, STREAM>;
 };
 
 template <typename T> struct Ones2;
@@ -610,7 +620,7 @@ constexpr size_t decode_lds_bytes() {
 // take the four 32-key blocks of each 128-key tile.
 template <typename T, int D, bool POW2>
 __global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
-    using Loader = typename LoaderSel<D, kDecTile, 4, POW2>::type;
+    using Loader = typename LoaderSel<D, kDecTile, 4, POW2, true>::type;
     constexpr int KP = Loader::KP, VP = Loader::VP;
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
 

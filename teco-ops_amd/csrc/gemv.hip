@@ -8,18 +8,22 @@
 // gfx950 design: batches of 3+ (fp16 / bf16) or 2+ (int8) rows of x with K a
 // multiple of 32 / 64 run on the matrix cores, see "MFMA path" below, in
 // slices of 16 columns.  Batch 1-2 (and other shapes) take the VALU path,
-// which streams W fastest when there is little math per byte: a workgroup of 4 waves owns 4*R consecutive output rows and
-// first stages x ([B, K], at most 64 KiB) in LDS.  Each wave streams R rows of
-// W with 16-byte loads, lane-interleaved along K so that every load
-// instruction reads a contiguous 1 KiB run of a row, and keeps R x B fp32
-// partial sums; the products use v_dot2_f32_{f16,bf16} (two MACs per
-// instruction, fp32 accumulation).  int8 weights are widened exactly to fp16
-// with one v_perm_b32 (bytes of w+128 under the exponent of 1024.0) and one
-// packed fp16 subtract of 1152 per weight pair.  A wave-wide xor-shuffle
+// which streams W fastest when there is little math per byte: a workgroup of 4
+// waves owns 4*R consecutive output rows and first stages x ([B, K], at most
+// 64 KiB) in LDS.  Each wave streams R rows of W with 16-byte loads,
+// lane-interleaved along K so that every load instruction reads a contiguous
+// 1 KiB run of a row; a lane issues the loads of CPL chunks of each row before
+// using any (a whole fp16 row, or two int8 rows, in flight per wave at K =
+// 4096), and keeps R x B fp32 partial sums; the products use
+// v_dot2_f32_{f16,bf16} (two MACs per instruction, fp32 accumulation).  int8
+// weights are widened exactly to fp16 with one v_perm_b32 (bytes of w+128
+// under the exponent of 1024.0) and one packed fp16 subtract of 1152 per
+// weight pair.  A wave-wide xor-shuffle
 // reduction finishes each (row, batch) sum; the per-row int8 scale is applied
 // to the fp32 sum.  HBM-bound: algorithmic bytes = |W| + |x| + |y| (+|s|).
 #include "common.h"
 #include "device.h"
+
 
 namespace {
 
@@ -56,72 +60,6 @@ __device__ __forceinline__ void stage_x(uint4 *xs, const uint4 *x, int nvec) {
     __syncthreads();
 }
 
-// W chunks kept in flight per row ahead of their use; the first ones are
-// issued before x is staged in LDS, so the barrier that publishes x does not
-// delay the weight stream.  One chunk measured best (deeper rings were slower).
-constexpr int kPrefetch = 1;
-
-template <typename T, int B, int R>
-__global__ void __launch_bounds__(kThreads)
-gemv16_kernel(const uint4 *__restrict__ W, const uint4 *__restrict__ x, uint16_t *__restrict__ y,
-              int N, int K) {
-    extern __shared__ uint4 xs[];
-    const int kv = K / 8;  // 16-byte chunks per row
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n0 = (blockIdx.x * kWaves + wave) * R;
-    const uint4 *wrow[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kv;
-    uint4 ring[kPrefetch][R];
-#pragma unroll
-    for (int i = 0; i < kPrefetch; ++i)
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            ring[i][r] = lane + 64 * i < kv ? load_stream(wrow[r] + lane + 64 * i) : uint4{};
-    stage_x(xs, x, B * kv);
-    if (n0 >= N) return;
-    float acc[R][B];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
-    for (int c0 = lane; c0 < kv; c0 += 64 * kPrefetch) {
-#pragma unroll
-        for (int i = 0; i < kPrefetch; ++i) {
-            const int c = c0 + 64 * i;
-            if (c < kv) {
-                uint4 wv[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    wv[r] = ring[i][r];
-                    const int cn = c + 64 * kPrefetch;
-                    if (cn < kv) ring[i][r] = load_stream(wrow[r] + cn);
-                }
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    const uint4 xv = xs[b * kv + c];
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float s = acc[r][b];
-                        s = Dot2<T>::run(wv[r].x, xv.x, s);
-                        s = Dot2<T>::run(wv[r].y, xv.y, s);
-                        s = Dot2<T>::run(wv[r].z, xv.z, s);
-                        s = Dot2<T>::run(wv[r].w, xv.w, s);
-                        acc[r][b] = s;
-                    }
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            const float s = wave_sum(acc[r][b]);
-            if (lane == 0 && n0 + r < N) y[static_cast<long long>(b) * N + n0 + r] = Cvt<T>::from(s);
-        }
-}
-
 // int8 weight dword (4 values) -> two packed fp16 pairs holding the exact values.
 __device__ __forceinline__ void widen_i8(uint32_t w, uint32_t &p01, uint32_t &p23) {
     const uint32_t u = w ^ 0x80808080u;  // bytes now hold w + 128 in [0, 255]
@@ -133,24 +71,28 @@ __device__ __forceinline__ void widen_i8(uint32_t w, uint32_t &p01, uint32_t &p2
     p23 = __builtin_bit_cast(uint32_t, h23 + bias);
 }
 
-template <int B, int R>
-__global__ void __launch_bounds__(kThreads)
+// int8 weights, VALU path with the weight loads batched: each K step of a
+// wave covers 64 * CPL 16-byte chunks of each of its R rows, and a lane issues
+// all R * CPL of its loads before widening any of them, so every lane keeps
+// R * CPL * 16 bytes in flight and a row needs K / (1024 * CPL) round trips.
+template <int B, int R, int CPL, int NW>
+__global__ void __launch_bounds__(NW * 64)
 gemv_i8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
-               const uint4 *__restrict__ x, uint16_t *__restrict__ y, int N, int K) {
+                       const uint4 *__restrict__ x, uint16_t *__restrict__ y, int N, int K) {
     extern __shared__ uint4 xs[];
     const int kx = K / 8;    // 16-byte chunks of an x row (8 fp16)
     const int kw = K / 16;   // 16-byte chunks of a W row (16 int8)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n0 = (blockIdx.x * kWaves + wave) * R;
+    const int n0 = (blockIdx.x * NW + wave) * R;
     const uint4 *wrow[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kw;
-    uint4 ring[kPrefetch][R];
+    uint4 q[R][CPL];
 #pragma unroll
-    for (int i = 0; i < kPrefetch; ++i)
+    for (int u = 0; u < CPL; ++u)
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            ring[i][r] = lane + 64 * i < kw ? load_stream(wrow[r] + lane + 64 * i) : uint4{};
+            q[r][u] = lane + 64 * u < kw ? load_stream(wrow[r] + lane + 64 * u) : uint4{};
     stage_x(xs, x, B * kx);
     if (n0 >= N) return;
     float acc[R][B];
@@ -158,37 +100,38 @@ gemv_i8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
-    for (int c0 = lane; c0 < kw; c0 += 64 * kPrefetch) {
+    for (int c0 = lane;; c0 += 64 * CPL) {
 #pragma unroll
-        for (int i = 0; i < kPrefetch; ++i) {
-            const int c = c0 + 64 * i;
+        for (int u = 0; u < CPL; ++u) {
+            const int c = c0 + 64 * u;
             if (c < kw) {
-                uint32_t wh[R][8];  // 16 weights as 8 fp16 pairs
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const uint4 q = ring[i][r];
-                    const int cn = c + 64 * kPrefetch;
-                    if (cn < kw) ring[i][r] = load_stream(wrow[r] + cn);
-                    widen_i8(q.x, wh[r][0], wh[r][1]);
-                    widen_i8(q.y, wh[r][2], wh[r][3]);
-                    widen_i8(q.z, wh[r][4], wh[r][5]);
-                    widen_i8(q.w, wh[r][6], wh[r][7]);
-                }
+                    uint32_t wh[8];  // 16 weights as 8 fp16 pairs
+                    widen_i8(q[r][u].x, wh[0], wh[1]);
+                    widen_i8(q[r][u].y, wh[2], wh[3]);
+                    widen_i8(q[r][u].z, wh[4], wh[5]);
+                    widen_i8(q[r][u].w, wh[6], wh[7]);
 #pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    const uint4 x0 = xs[b * kx + 2 * c];
-                    const uint4 x1 = xs[b * kx + 2 * c + 1];
-                    const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
+                    for (int b = 0; b < B; ++b) {
+                        const uint4 x0 = xs[b * kx + 2 * c];
+                        const uint4 x1 = xs[b * kx + 2 * c + 1];
+                        const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
                         float s = acc[r][b];
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) s = Dot2<f16>::run(wh[r][j], xv[j], s);
+                        for (int j = 0; j < 8; ++j) s = Dot2<f16>::run(wh[j], xv[j], s);
                         acc[r][b] = s;
                     }
                 }
             }
         }
+        const int cn = c0 + 64 * CPL;
+        if (cn - lane >= kw) break;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (cn + 64 * u < kw) q[r][u] = load_stream(wrow[r] + cn + 64 * u);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -199,6 +142,68 @@ gemv_i8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
             if (lane == 0 && n0 + r < N) y[static_cast<long long>(b) * N + n0 + r] = f2h(sc * s);
         }
     }
+}
+
+// fp16 / bf16 weights, VALU path with batched loads (as gemv_i8_kernel).
+template <typename T, int B, int R, int CPL, int NW>
+__global__ void __launch_bounds__(NW * 64)
+gemv16_kernel(const uint4 *__restrict__ W, const uint4 *__restrict__ x,
+                      uint16_t *__restrict__ y, int N, int K) {
+    extern __shared__ uint4 xs[];
+    const int kv = K / 8;  // 16-byte chunks per row
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * NW + wave) * R;
+    const uint4 *wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kv;
+    uint4 q[R][CPL];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            q[r][u] = lane + 64 * u < kv ? load_stream(wrow[r] + lane + 64 * u) : uint4{};
+    stage_x(xs, x, B * kv);
+    if (n0 >= N) return;
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
+    for (int c0 = lane;; c0 += 64 * CPL) {
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+            const int c = c0 + 64 * u;
+            if (c < kv) {
+#pragma unroll
+                for (int b = 0; b < B; ++b) {
+                    const uint4 xv = xs[b * kv + c];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float s = acc[r][b];
+                        s = Dot2<T>::run(q[r][u].x, xv.x, s);
+                        s = Dot2<T>::run(q[r][u].y, xv.y, s);
+                        s = Dot2<T>::run(q[r][u].z, xv.z, s);
+                        s = Dot2<T>::run(q[r][u].w, xv.w, s);
+                        acc[r][b] = s;
+                    }
+                }
+            }
+        }
+        const int cn = c0 + 64 * CPL;
+        if (cn - lane >= kv) break;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (cn + 64 * u < kv) q[r][u] = load_stream(wrow[r] + cn + 64 * u);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float s = wave_sum(acc[r][b]);
+            if (lane == 0 && n0 + r < N) y[static_cast<long long>(b) * N + n0 + r] = Cvt<T>::from(s);
+        }
 }
 
 // ------------------------------------------------------------------ MFMA path
@@ -434,23 +439,31 @@ constexpr int kMaxLdsBytes = 64 * 1024;
 constexpr int kMfmaMinBatch16 = 3, kMfmaRT16 = 1, kMfmaWaves16 = 4;
 constexpr int kMfmaMinBatchI8 = 2, kMfmaRTI8 = 4, kMfmaWavesI8 = 8;
 
+// VALU path shapes (rows per wave R, 16-byte W chunks per lane per K step
+// CPL), measured on the [14336, 4096] batch-1 shapes: fp16 one row per wave
+// with the whole 8 KiB row in flight (19.5 us; 4 rows with one chunk in
+// flight: 22.6 us), int8 two 4 KiB rows per wave (12.9 us; 15.5 us before).
+// Fewer rows per wave beat deeper per-wave queues: 4 rows x 4 chunks of int8
+// took 16.2 us, and 8 or 16 waves per workgroup were slower for both types.
+constexpr int kR16 = 1, kCpl16 = 8;
+constexpr int kRI8 = 2, kCplI8 = 4;
+
 template <typename T, int B>
 void launch16(const void *W, const void *x, void *y, int N, int K, hipStream_t s) {
-    constexpr int R = 4;
-    const unsigned grid = tecoops::ceil_div(N, kWaves * R);
-    hipLaunchKernelGGL((gemv16_kernel<T, B, R>), dim3(grid), dim3(kThreads), B * K * 2, s,
-                       static_cast<const uint4 *>(W), static_cast<const uint4 *>(x),
+    const unsigned grid = tecoops::ceil_div(N, kWaves * kR16);
+    hipLaunchKernelGGL((gemv16_kernel<T, B, kR16, kCpl16, kWaves>), dim3(grid), dim3(kThreads),
+                       B * K * 2, s, static_cast<const uint4 *>(W), static_cast<const uint4 *>(x),
                        static_cast<uint16_t *>(y), N, K);
 }
 
 template <int B>
 void launch_i8(const void *W, const void *sc, const void *x, void *y, int N, int K,
                hipStream_t s) {
-    constexpr int R = 4;
-    const unsigned grid = tecoops::ceil_div(N, kWaves * R);
-    hipLaunchKernelGGL((gemv_i8_kernel<B, R>), dim3(grid), dim3(kThreads), B * K * 2, s,
-                       static_cast<const uint4 *>(W), static_cast<const uint16_t *>(sc),
-                       static_cast<const uint4 *>(x), static_cast<uint16_t *>(y), N, K);
+    const unsigned grid = tecoops::ceil_div(N, kWaves * kRI8);
+    hipLaunchKernelGGL((gemv_i8_kernel<B, kRI8, kCplI8, kWaves>), dim3(grid), dim3(kThreads),
+                       B * K * 2, s, static_cast<const uint4 *>(W),
+                       static_cast<const uint16_t *>(sc), static_cast<const uint4 *>(x),
+                       static_cast<uint16_t *>(y), N, K);
 }
 
 template <typename T>
