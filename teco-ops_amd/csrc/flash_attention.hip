@@ -821,9 +821,12 @@ Plan make_plan(int batch, int H, int Hkv, int max_q, int max_k) {
     pl.decode = max_q >= 1 && G * max_q <= 32;
     pl.rq = max_q;
     pl.ncols = G * max_q;
-    // Split the key range so that the grid has at least ~2048 workgroups.
+    // Split the key range so that the grid has at least ~2048 workgroups, with
+    // splits as long as that allows (up to 2048 keys): at B=64, Hkv=8 and
+    // kv_len <= 8192, 2048-key splits ran in 194 us against 217 us at 512
+    // (fewer partials to write and merge; the merge kernel is a fixed cost).
     const long long units = static_cast<long long>(batch) * Hkv;
-    int split = 512;
+    int split = 2048;
     while (split > kDecTile && units * ((max_k + split - 1) / split) < 2048) split >>= 1;
     pl.split_len = split;
     pl.max_splits = max_k <= 0 ? 1 : (max_k + split - 1) / split;
