@@ -159,8 +159,11 @@ __device__ __forceinline__ void conv1d_body(const ConvArgs &a, int b, int d, int
 // the carried last values of the previous group of segments, or the prefix
 // (old conv state or zeros), at the start of a row.  A workgroup of 4 waves
 // takes 4 * kRowsPerWave consecutive rows.  Token stride is 1 (x and out).
+// One row per wave: at [8, 4096, 2048] that is 32768 short-lived waves, which
+// keep reads and writes of different waves overlapped (47.5 us); 4 rows per
+// wave made the resident waves load, compute and store in lockstep (58.3 us).
 constexpr int kSegs = 4;
-constexpr int kRowsPerWave = 4;
+constexpr int kRowsPerWave = 1;
 
 template <int W>
 __global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {

@@ -7,52 +7,66 @@
 //   key_cache[blk][h][off][:] = key[t][h][:]   (and value likewise)
 // for every kv head h.  The copy is bit-exact.
 //
-// gfx950 design: one lane per 16-byte chunk of a (token, head) row; a wave
-// covers 1 KiB of contiguous key (and value) bytes, so reads are fully
-// coalesced and every destination run is a whole head_size row.  Each lane
-// moves one key and one value chunk (the access shape that streams fastest
-// on MI355X: one 16-byte vector per lane over a large grid).
+// gfx950 design: 16-byte chunks of (token, head) rows; each load instruction
+// of a wave covers 1 KiB of contiguous key (and value) bytes, so reads are
+// fully coalesced and every destination run is a whole head_size row.  Each
+// lane moves 8 key and 8 value chunks with every load in flight before the
+// first store (non-temporal, read and written once).
 // HBM-bound: algorithmic bytes = 4 * num_tokens * H * D * 2 + 8 * num_tokens.
 #include "common.h"
 #include "device.h"
 
+
 namespace {
 
-// One lane per chunk (16 bytes when aligned) of one (token, head) row, key
-// and value, over a 1-D grid of num_tokens * per_token lanes (per launch
-// slice): every lane moves data whatever heads * head_size is.  Slot arithmetic
-// is 32-bit (slots < 2^31 after the range check), with a shift / mask when
-// block_size is a power of two.  Key and value are streamed (non-temporal).
-template <typename V, bool POW2>
+// Each lane moves U chunks (16 bytes when aligned) of (token, head) rows, key
+// and value, spaced 256 chunks apart over a 1-D grid of num_tokens * per_token
+// chunks (per launch slice), so every lane moves data whatever heads *
+// head_size is; all U key / value / slot loads are issued before the
+// scattered stores.  Slot arithmetic is 32-bit (slots < 2^31 after the range
+// check), with a shift / mask when block_size is a power of two.  Key and
+// value are streamed (non-temporal).
+template <typename V, bool POW2, int U>
 __global__ void __launch_bounds__(256)
 reshape_and_cache_kernel(const V *__restrict__ key, const V *__restrict__ value,
                          const int64_t *__restrict__ slot_mapping, V *__restrict__ key_cache,
                          V *__restrict__ value_cache, int heads, int vec_per_row, int block_size,
                          int lbs, long long capacity, int total) {
-    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= total) return;
     const int per_token = heads * vec_per_row;
-    const int t = gid / per_token;
-    const int rem = gid - t * per_token;
-    const int64_t slot = slot_mapping[t];
-    const V kv = tecoops::dev::ld_stream(key + gid);
-    const V vv = tecoops::dev::ld_stream(value + gid);
-    if (slot < 0 || slot >= capacity) return;
-    const int s32 = static_cast<int>(slot);
-    int blk, off;
-    if (POW2) {
-        blk = s32 >> lbs;
-        off = s32 & (block_size - 1);
-    } else {
-        blk = s32 / block_size;
-        off = s32 - blk * block_size;
+    const int g0 = blockIdx.x * (256 * U) + threadIdx.x;
+    V kv[U], vv[U];
+    int64_t slot[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int gid = g0 + 256 * u;
+        if (gid < total) {
+            kv[u] = tecoops::dev::ld_stream(key + gid);
+            vv[u] = tecoops::dev::ld_stream(value + gid);
+            slot[u] = slot_mapping[gid / per_token];
+        }
     }
-    const int h = rem / vec_per_row;
-    const int c = rem - h * vec_per_row;
-    const long long dst =
-        ((static_cast<long long>(blk) * heads + h) * block_size + off) * vec_per_row + c;
-    tecoops::dev::st_stream(key_cache + dst, kv);
-    tecoops::dev::st_stream(value_cache + dst, vv);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int gid = g0 + 256 * u;
+        if (gid >= total || slot[u] < 0 || slot[u] >= capacity) continue;
+        const int t = gid / per_token;
+        const int rem = gid - t * per_token;
+        const int s32 = static_cast<int>(slot[u]);
+        int blk, off;
+        if (POW2) {
+            blk = s32 >> lbs;
+            off = s32 & (block_size - 1);
+        } else {
+            blk = s32 / block_size;
+            off = s32 - blk * block_size;
+        }
+        const int h = rem / vec_per_row;
+        const int c = rem - h * vec_per_row;
+        const long long dst =
+            ((static_cast<long long>(blk) * heads + h) * block_size + off) * vec_per_row + c;
+        tecoops::dev::st_stream(key_cache + dst, kv[u]);
+        tecoops::dev::st_stream(value_cache + dst, vv[u]);
+    }
 }
 
 template <typename V>
@@ -67,14 +81,17 @@ tecoopsStatus_t launch(tecoopsHandle_t handle, const void *key, const void *valu
         return TECOOPS_STATUS_NOT_SUPPORTED;
     }
     const int lbs = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
-    auto *kern = lbs >= 0 ? &reshape_and_cache_kernel<V, true> : &reshape_and_cache_kernel<V, false>;
+    // 8 chunks per lane, all loaded before the scattered stores: 12.6 us at
+    // 8192 tokens x 8 heads x 128 (14.9 us with one chunk per lane)
+    constexpr int U = 8;
+    auto *kern = lbs >= 0 ? &reshape_and_cache_kernel<V, true, U> : &reshape_and_cache_kernel<V, false, U>;
     // lane indices are 32-bit: tokens run in slices of fewer than 2^30 lanes
     const int slice = static_cast<int>((1ll << 30) / per_token);
     for (int t0 = 0; t0 < num_tokens; t0 += slice) {
         const int nt = num_tokens - t0 < slice ? num_tokens - t0 : slice;
         const int total = static_cast<int>(per_token * nt);
         const long long src0 = static_cast<long long>(t0) * per_token;
-        hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(total, 256)), dim3(256), 0, handle->stream,
+        hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(total, 256 * U)), dim3(256), 0, handle->stream,
                            static_cast<const V *>(key) + src0, static_cast<const V *>(value) + src0,
                            slot_mapping + t0, static_cast<V *>(key_cache),
                            static_cast<V *>(value_cache), heads, vec_per_row, block_size, lbs,
