@@ -5,22 +5,27 @@
 //   fp16 / bf16:  y[b, n] = T( sum_k W[n, k] * x[b, k] )            fp32 acc
 //   int8:         y[b, n] = fp16( s[n] * sum_k float(Wq[n, k]) * x[b, k] )
 //
-// gfx950 design: batches of 3+ (fp16 / bf16) or 2+ (int8) rows of x with K a
-// multiple of 32 / 64 run on the matrix cores, see "MFMA path" below, in
-// slices of 16 columns.  Batch 1-2 (and other shapes) take the VALU path,
-// which streams W fastest when there is little math per byte: a workgroup of 4
-// waves owns 4*R consecutive output rows and first stages x ([B, K], at most
-// 64 KiB) in LDS.  Each wave streams R rows of W with 16-byte loads,
-// lane-interleaved along K so that every load instruction reads a contiguous
-// 1 KiB run of a row; a lane issues the loads of CPL chunks of each row before
-// using any (a whole fp16 row, or two int8 rows, in flight per wave at K =
-// 4096), and keeps R x B fp32 partial sums; the products use
-// v_dot2_f32_{f16,bf16} (two MACs per instruction, fp32 accumulation).  int8
-// weights are widened exactly to fp16 with one v_perm_b32 (bytes of w+128
-// under the exponent of 1024.0) and one packed fp16 subtract of 1152 per
-// weight pair.  A wave-wide xor-shuffle
-// reduction finishes each (row, batch) sum; the per-row int8 scale is applied
-// to the fp32 sum.  HBM-bound: algorithmic bytes = |W| + |x| + |y| (+|s|).
+// gfx950 design, by batch size (rows of x):
+//   * 3-8 (fp16 / bf16) or 2-8 (int8) with K a multiple of 128 / 256: the
+//     4x4x4 matrix-core path ("4x4x4 MFMA path" below).  Each wave streams 4
+//     whole rows of W in 256-byte row segments, x sits in LDS, and the waves
+//     start their sweeps of K at staggered offsets.
+//   * larger batches and other K (multiples of 32 / 64): the 16x16x32
+//     matrix-core path ("MFMA path" below), in slices of 16 columns.
+//   * 1-2 and all other shapes: the VALU path, which streams W fastest when
+//     there is little math per byte.  A workgroup of 4 waves owns 4*R
+//     consecutive output rows and first stages x ([B, K], at most 64 KiB) in
+//     LDS.  Each wave streams R rows of W with 16-byte loads, lane-interleaved
+//     along K so that every load instruction reads a contiguous 1 KiB run of
+//     a row; a lane issues the loads of CPL chunks of each row before using
+//     any (a whole fp16 row, or two int8 rows, in flight per wave at K =
+//     4096), and keeps R x B fp32 partial sums; the products use
+//     v_dot2_f32_{f16,bf16} (two MACs per instruction, fp32 accumulation).  A
+//     wave-wide xor-shuffle reduction finishes each (row, batch) sum.
+// int8 weights are widened exactly to fp16 with one v_perm_b32 (bytes of
+// w+128 under the exponent of 1024.0) and one packed fp16 subtract of 1152 per
+// weight pair; the per-row int8 scale is applied to the fp32 sum.
+// HBM-bound: algorithmic bytes = |W| + |x| + |y| (+|s|).
 #include "common.h"
 #include "device.h"
 
@@ -273,33 +278,32 @@ __device__ __forceinline__ void gemv_mfma_epilogue(f32x4_t (&c)[RT], float *red,
     }
 }
 
-// Runs one wave's n split-K steps (n wave-uniform) with the loads of each step
-// issued kRing steps ahead of its MFMAs: load(j, i) fetches step j into ring
-// slot i and use(i) consumes slot i.  Slot indices are compile-time constants
-// after unrolling, so the ring stays in registers and the waits before each
-// use leave the younger loads in flight.  Measured on the [14336, 4096]
-// batch-8 shapes, deeper rings do not pay: the fp16 kernel goes from 29 us at
-// depth 1 to 33 us at depth 4 (each load instruction already touches 16 rows
-// and the workgroups keep enough requests in flight), int8 with 4 row tiles
-// is flat (17.0 / 17.2 / 17.3 us at depths 1 / 2 / 4).
-constexpr int kRing = 1;
-
-template <int D, typename Load, typename Use>
-__device__ __forceinline__ void ring_steps(int n, Load &&load, Use &&use) {
+// Runs one wave's n steps (n wave-uniform) with the loads of each step issued
+// D steps ahead of its use: load(j, i) fetches step j into ring slot i and
+// use(j, i) consumes step j from slot i; start() runs once, after the first
+// loads are issued and before the first use.  Slot indices are compile-time
+// constants after unrolling, so the ring stays in registers, and the loads of
+// the main loop are unconditional, so the waits before each use leave the
+// younger loads in flight.
+template <int D, typename Load, typename Use, typename Start>
+__device__ __forceinline__ void ring_steps(int n, Load &&load, Use &&use, Start &&start) {
     if (n < D) {
         for (int j = 0; j < n; ++j) {
             load(j, 0);
-            use(0);
+            if (j == 0) start();
+            use(j, 0);
         }
+        if (n <= 0) start();
         return;
     }
 #pragma unroll
     for (int i = 0; i < D; ++i) load(i, i);
+    start();
     int j = 0;
     for (; j + 2 * D <= n; j += D) {
 #pragma unroll
         for (int i = 0; i < D; ++i) {
-            use(i);
+            use(j + i, i);
             load(j + D + i, i);
             // keep this order: the scheduler would otherwise batch the loads
             // at the end of the iteration and drain the ring at its top
@@ -309,13 +313,25 @@ __device__ __forceinline__ void ring_steps(int n, Load &&load, Use &&use) {
     // steps j .. j+D-1 are in the ring; j+D .. n-1 (fewer than D) are not
 #pragma unroll
     for (int i = 0; i < D; ++i) {
-        use(i);
+        use(j + i, i);
         if (j + D + i < n) load(j + D + i, i);
     }
 #pragma unroll
     for (int i = 0; i < D; ++i)
-        if (j + D + i < n) use(i);
+        if (j + D + i < n) use(j + D + i, i);
 }
+
+template <int D, typename Load, typename Use>
+__device__ __forceinline__ void ring_steps(int n, Load &&load, Use &&use) {
+    ring_steps<D>(n, load, use, [] {});
+}
+
+// Depth of the 16x16x32 kernels' ring.  Measured on the [14336, 4096]
+// batch-8 shapes, deeper rings do not pay: the fp16 kernel goes from 29 us at
+// depth 1 to 33 us at depth 4 (each load instruction already touches 16 rows
+// and the workgroups keep enough requests in flight), int8 with 4 row tiles
+// is flat (17.0 / 17.2 / 17.3 us at depths 1 / 2 / 4).
+constexpr int kRing = 1;
 
 // Wave w takes the 32-k (16-bit W) or 64-k (int8 W) steps w, w+4, w+8, ...
 // Columns >= B of the B operand read row B-1 of x: the C columns they produce
@@ -347,7 +363,7 @@ gemv16_mfma_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ 
             for (int rt = 0; rt < RT; ++rt) a[i][rt] = ld16_stream(wr[rt] + k0);
             b[i] = ld16(xr + k0);
         },
-        [&](int i) {
+        [&](int, int i) {
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) c[rt] = Mma16<T>::run(a[i][rt], b[i], c[rt]);
         });
@@ -393,7 +409,7 @@ gemv_i8_mfma_kernel(const int8_t *__restrict__ W, const uint16_t *__restrict__ s
             b0[i] = ld16(xr + k0);
             b1[i] = ld16(xr + k0 + 8);
         },
-        [&](int i) {
+        [&](int, int i) {
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
                 u32x4_t a0, a1;
@@ -403,6 +419,195 @@ gemv_i8_mfma_kernel(const int8_t *__restrict__ W, const uint16_t *__restrict__ s
             }
         });
     gemv_mfma_epilogue<f16, RT, NW>(c, red, n0, N, B, y, scales);
+}
+
+// ------------------------------------------------------ 4x4x4 MFMA path
+//
+// Batches of up to 8 rows of x: Y^T = W X^T on v_mfma_f32_4x4x4_16b_{f16,
+// bf16}, which runs 16 independent 4x4x4 products (blocks) per instruction.
+// Lane l = 4*blk + r supplies row r of block blk's A operand and column r of
+// its B operand, and receives column r of its C block.  Each wave owns 4 whole
+// rows of W: lane l loads the 16 bytes at chunk blk of every 16-chunk
+// (256-byte) run of row n0 + r, so one load instruction reads four contiguous
+// 256-byte row segments (the access pattern of the VALU path), and block blk
+// accumulates those 4 rows against batch columns 4*cg + r over its own k
+// values.  The 16 blocks hold partial sums over disjoint k; a butterfly over
+// lanes l ^ 4, ^ 8, ^ 16, ^ 32 adds them once the wave has covered K.  No
+// cross-wave reduction or barrier follows the staging of x.
+//   x is staged in LDS as [4*NCG][K] 16-bit values with the 16-byte chunks of
+//   row i XOR-swizzled by 4*(i % 4) inside each 256-byte run, so that the
+//   128-bit B-operand reads of lanes 0-7 (rows 0-3, two chunks) hit distinct
+//   banks.  int8 weights are widened exactly to fp16 (widen_i8) and feed 4
+//   k-steps per 16-byte load; the per-row scale is applied to the fp32 sum.
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+
+template <typename T> struct Mma4;
+template <> struct Mma4<f16> {
+    static __device__ __forceinline__ f32x4_t run(uint32_t a0, uint32_t a1, uint32_t b0,
+                                                  uint32_t b1, f32x4_t c) {
+        const u32x2_t a = {a0, a1}, b = {b0, b1};
+        return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4_t, a),
+                                                  __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+    }
+};
+template <> struct Mma4<bf16> {
+    static __device__ __forceinline__ f32x4_t run(uint32_t a0, uint32_t a1, uint32_t b0,
+                                                  uint32_t b1, f32x4_t c) {
+        const u32x2_t a = {a0, a1}, b = {b0, b1};
+        return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(i16x4_t, a),
+                                                      __builtin_bit_cast(i16x4_t, b), c, 0, 0, 0);
+    }
+};
+
+// Staged x is at most 64 KiB: 4096 16-byte chunks.
+constexpr int kMaxXChunks = 4096;
+
+// LDS element offset of the 16-byte chunk c of staged x row `row`.
+__device__ __forceinline__ int xs_chunk(int row, int c, int K) {
+    return row * K + 8 * (c ^ (4 * (row & 3)));
+}
+
+// T: element type of x / y (and W unless I8).  NCG: batch column groups of 4
+// (1 for B <= 4, else 2).  RG: groups of 4 rows per wave, which share each x
+// read from LDS.  CPL: load steps a lane keeps in flight (RG loads each).
+template <typename T, bool I8, int NCG, int RG, int NW, int CPL>
+__global__ void __launch_bounds__(NW * 64)
+gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
+               const uint4 *__restrict__ x, uint16_t *__restrict__ y, int N, int K, int B) {
+    extern __shared__ uint4 xs_raw[];
+    uint16_t *xs = reinterpret_cast<uint16_t *>(xs_raw);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 3, blk = lane >> 2;
+    const int n0 = (blockIdx.x * NW + wave) * 4 * RG;
+    const int kw = I8 ? K / 16 : K / 8;  // 16-byte chunks of a W row
+    const int nl = kw / 16;              // load steps per row
+    const uint4 *wr[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+        wr[g] = W + static_cast<long long>(min(n0 + 4 * g + r, N - 1)) * kw + blk;
+    const int kx = K / 8;  // 16-byte chunks of an x row
+    f32x4_t acc[RG][NCG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) acc[g][cg] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // The x loads are issued first (unconditionally, clamped to the last
+    // chunk), so that waiting for them leaves the younger W loads in flight.
+    constexpr int XPT = kMaxXChunks / (NW * 64);  // x chunks per thread
+    const int nxc = NCG * 4 * kx;
+    uint4 xr[XPT];
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+        const int idx = min(static_cast<int>(threadIdx.x) + j * NW * 64, nxc - 1);
+        const int row = min(idx / kx, B - 1);
+        xr[j] = x[static_cast<long long>(row) * kx + idx % kx];
+    }
+    uint4 q[CPL][RG];
+    // Each wave starts its sweep of K at a different load step, so that the
+    // requests in flight across the grid spread over all HBM channels instead
+    // of every wave reading the same offset of its rows at the same time.
+    const int rot = (blockIdx.x * NW + wave) % nl;
+    const auto step = [&](int i) { return i + rot < nl ? i + rot : i + rot - nl; };
+    // Waves past the last row still stage x and reach the barrier; their
+    // loads read row N - 1 and their sums are never stored.
+    ring_steps<CPL>(
+        nl,
+        [&](int i, int u) {
+            const int st = 16 * step(i);
+#pragma unroll
+            for (int g = 0; g < RG; ++g) q[u][g] = load_stream(wr[g] + st);
+        },
+        [&](int i0, int u) {
+            const int i = step(i0);
+            if constexpr (I8) {
+                uint32_t p[RG][8];
+#pragma unroll
+                for (int g = 0; g < RG; ++g) {
+                    widen_i8(q[u][g].x, p[g][0], p[g][1]);
+                    widen_i8(q[u][g].y, p[g][2], p[g][3]);
+                    widen_i8(q[u][g].z, p[g][4], p[g][5]);
+                    widen_i8(q[u][g].w, p[g][6], p[g][7]);
+                }
+#pragma unroll
+                for (int cg = 0; cg < NCG; ++cg) {
+                    const int row = 4 * cg + r;
+                    const uint4 xa = *reinterpret_cast<const uint4 *>(
+                        xs + xs_chunk(row, 32 * i + 2 * blk, K));
+                    const uint4 xb = *reinterpret_cast<const uint4 *>(
+                        xs + xs_chunk(row, 32 * i + 2 * blk + 1, K));
+#pragma unroll
+                    for (int g = 0; g < RG; ++g) {
+                        f32x4_t c = acc[g][cg];
+                        c = Mma4<f16>::run(p[g][0], p[g][1], xa.x, xa.y, c);
+                        c = Mma4<f16>::run(p[g][2], p[g][3], xa.z, xa.w, c);
+                        c = Mma4<f16>::run(p[g][4], p[g][5], xb.x, xb.y, c);
+                        c = Mma4<f16>::run(p[g][6], p[g][7], xb.z, xb.w, c);
+                        acc[g][cg] = c;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int cg = 0; cg < NCG; ++cg) {
+                    const uint4 xv = *reinterpret_cast<const uint4 *>(
+                        xs + xs_chunk(4 * cg + r, 16 * i + blk, K));
+#pragma unroll
+                    for (int g = 0; g < RG; ++g) {
+                        acc[g][cg] = Mma4<T>::run(q[u][g].x, q[u][g].y, xv.x, xv.y, acc[g][cg]);
+                        acc[g][cg] = Mma4<T>::run(q[u][g].z, q[u][g].w, xv.z, xv.w, acc[g][cg]);
+                    }
+                }
+            }
+        },
+        // the x chunks reach LDS once the first W loads are in flight
+        [&] {
+#pragma unroll
+            for (int j = 0; j < XPT; ++j) {
+                const int idx = threadIdx.x + j * NW * 64;
+                if (idx < nxc) {
+                    const int row = idx / kx, c = idx - row * kx;
+                    *reinterpret_cast<uint4 *>(xs + xs_chunk(row, c, K)) =
+                        row < B ? xr[j] : uint4{0u, 0u, 0u, 0u};
+                }
+            }
+            __syncthreads();
+        });
+    if (n0 >= N) return;
+    // add the 16 blocks' partial sums; lanes 0-3 then hold column r of rows
+    // n0 + 4g .. n0 + 4g + 3
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                float t = acc[g][cg][v];
+                t += __shfl_xor(t, 4, 64);
+                t += __shfl_xor(t, 8, 64);
+                t += __shfl_xor(t, 16, 64);
+                t += __shfl_xor(t, 32, 64);
+                acc[g][cg][v] = t;
+            }
+    if (blk == 0) {
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg) {
+                const int b = 4 * cg + r;
+                if (b < B) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int n = n0 + 4 * g + v;
+                        if (n < N) {
+                            const float o = I8 ? acc[g][cg][v] * h2f(scales[n]) : acc[g][cg][v];
+                            y[static_cast<long long>(b) * N + n] = Cvt<T>::from(o);
+                        }
+                    }
+                }
+            }
+    }
 }
 
 // Fallback for shapes the vector kernels do not take (K not a multiple of 8 /
@@ -447,6 +652,35 @@ constexpr int kMfmaMinBatchI8 = 2, kMfmaRTI8 = 4, kMfmaWavesI8 = 8;
 // took 16.2 us, and 8 or 16 waves per workgroup were slower for both types.
 constexpr int kR16 = 1, kCpl16 = 8;
 constexpr int kRI8 = 2, kCplI8 = 4;
+
+// 4x4x4 path: waves per workgroup (x is staged once per workgroup), groups
+// of 4 rows per wave and load steps in flight per lane, for fp16 / int8 W.
+// x fills at most 64 KiB of LDS.
+constexpr int kB8Waves = 16, kB8RgF16 = 1, kB8CplF16 = 8, kB8RgI8 = 1, kB8CplI8 = 4;
+constexpr int kB8MaxBatch = 8;
+
+bool b8_fits(int batch, int k, bool i8) {
+    if (batch > kB8MaxBatch || k % (i8 ? 256 : 128) != 0) return false;
+    return static_cast<long long>(batch <= 4 ? 4 : 8) * k * 2 <= kMaxLdsBytes;
+}
+
+template <typename T, bool I8>
+void launch_b8(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
+               hipStream_t s) {
+    constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
+    constexpr int CPL = I8 ? kB8CplI8 : kB8CplF16;
+    const unsigned grid = tecoops::ceil_div(N, 4 * RG * kB8Waves);
+    const uint4 *w4 = static_cast<const uint4 *>(W);
+    const uint16_t *s16 = static_cast<const uint16_t *>(sc);
+    const uint4 *x4 = static_cast<const uint4 *>(x);
+    uint16_t *y16 = static_cast<uint16_t *>(y);
+    if (B <= 4)
+        hipLaunchKernelGGL((gemv_b8_kernel<T, I8, 1, RG, kB8Waves, CPL>), dim3(grid),
+                           dim3(kB8Waves * 64), 4 * K * 2, s, w4, s16, x4, y16, N, K, B);
+    else
+        hipLaunchKernelGGL((gemv_b8_kernel<T, I8, 2, RG, kB8Waves, CPL>), dim3(grid),
+                           dim3(kB8Waves * 64), 8 * K * 2, s, w4, s16, x4, y16, N, K, B);
+}
 
 template <typename T, int B>
 void launch16(const void *W, const void *x, void *y, int N, int K, hipStream_t s) {
@@ -506,6 +740,15 @@ extern "C" tecoopsStatus_t tecoopsGemv(tecoopsHandle_t handle, const void *weigh
     using tecoops::dev::bf16;
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
+    if (batch >= kMfmaMinBatch16 && b8_fits(batch, k, false) && tecoops::aligned(weight, 16) &&
+        tecoops::aligned(x, 16)) {
+        if (dataType == TECOOPS_DATA_HALF)
+            launch_b8<f16, false>(weight, nullptr, x, y, batch, n, k, s);
+        else
+            launch_b8<bf16, false>(weight, nullptr, x, y, batch, n, k, s);
+        TECO_CHECK_LAUNCH("gemv");
+        return TECOOPS_STATUS_SUCCESS;
+    }
     if (batch >= kMfmaMinBatch16 && (k % 32) == 0 && tecoops::aligned(weight, 16) &&
         tecoops::aligned(x, 16)) {
         constexpr int RT = kMfmaRT16, NW = kMfmaWaves16;
@@ -560,6 +803,12 @@ extern "C" tecoopsStatus_t tecoopsGemvInt8(tecoopsHandle_t handle, const int8_t 
     if (batch <= 0 || n <= 0 || k <= 0) return TECOOPS_STATUS_BAD_PARAM;
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
+    if (batch >= kMfmaMinBatchI8 && b8_fits(batch, k, true) && tecoops::aligned(weight, 16) &&
+        tecoops::aligned(x, 16)) {
+        launch_b8<f16, true>(weight, scales, x, y, batch, n, k, s);
+        TECO_CHECK_LAUNCH("gemv_int8");
+        return TECOOPS_STATUS_SUCCESS;
+    }
     if (batch >= kMfmaMinBatchI8 && (k % 64) == 0 && tecoops::aligned(weight, 16) &&
         tecoops::aligned(x, 16)) {
         constexpr int RT = kMfmaRTI8, NW = kMfmaWavesI8;

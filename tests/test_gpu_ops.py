@@ -437,6 +437,42 @@ def test_gemv_int8_matrix_core_ragged_k(K):
                  what=f"gemv_int8 3x{N}x{K}")
 
 
+@pytest.mark.parametrize("B,K,dt", [(4, 128, orc.HALF), (6, 1152, orc.BF16),
+                                    (8, 2944, orc.HALF), (3, 4096, orc.BF16)])
+def test_gemv_small_batch_matrix_core(B, K, dt):
+    """Batches 3-8 with K % 128 == 0 run the 4x4x4 path: each wave streams 4
+    rows with 8 loads in flight.  K = 128 is one load per row (fewer than the
+    ring depth), 1152 and 2944 are 9 and 23 loads (not multiples of it); N =
+    301 leaves a partial row group and waves past the last row."""
+    r = rng(800 + K + B)
+    N = 301
+    W = bits(r.normal(0, 0.05, (N, K)), dt)
+    x = bits(r.standard_normal((B, K)), dt)
+    ref = orc.gemv(W, x, dtype=dt)
+    y = torch.empty((B, N), dtype=torch.float16 if dt == orc.HALF else torch.bfloat16,
+                    device="cuda")
+    tecoops.gemv(dev(W, dt), dev(x, dt), y)
+    torch.cuda.synchronize()
+    assert_close(as_f32(y, dt), ref, what=f"gemv {B}x{N}x{K}")
+
+
+@pytest.mark.parametrize("B,K", [(2, 256), (7, 2304), (4, 4096), (8, 768)])
+def test_gemv_int8_small_batch_matrix_core(B, K):
+    """int8 batches 2-8 with K % 256 == 0 take the 4x4x4 path: 1, 9, 16 and 3
+    loads per row."""
+    r = rng(900 + K + B)
+    N = 203
+    W = r.integers(-127, 128, (N, K), dtype=np.int8)
+    s = bits(r.uniform(0.001, 0.01, N))
+    x = bits(r.standard_normal((B, K)))
+    ref = orc.gemv_int8(W, s, x)
+    y = torch.empty((B, N), dtype=torch.float16, device="cuda")
+    tecoops.gemv_int8(dev(W), dev(s), dev(x), y)
+    torch.cuda.synchronize()
+    assert_close(as_f32(y), ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2,
+                 what=f"gemv_int8 {B}x{N}x{K}")
+
+
 def test_gemv_odd_shapes_and_bf16():
     r = rng(500)
     for N, K, dt in ((33, 100, orc.HALF), (64, 4096, orc.BF16)):
