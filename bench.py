@@ -56,8 +56,8 @@ FA_PREFILL_FLOP = 4 * FA_B * FA_H * FA_D * FA_S * (FA_S + 1) // 2
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--ops", default="")
     ap.add_argument("--cpu-threads", type=int, default=0)
