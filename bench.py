@@ -27,7 +27,9 @@ FLOP count / average kernel time), the throughput figure of BASELINE.json's
 metric; `ops` lists every op's microseconds, algorithmic GB/s or TFLOP/s and
 fraction of the MI355X peak.  `roofline` is the dominant kernel's (by time).
 `cpu_baseline` times the CPU oracle (the reference algorithms restated in C)
-on the host cores on a bounded sample.
+on the host cores on a bounded sample of the FA prefill config, with a
+single-thread figure beside it; `cpu_ops` times the oracle on every other op
+at its full config.  Both are reported baselines, not targets.
 """
 import argparse
 import json
@@ -289,6 +291,112 @@ def cpu_baseline(threads, budget_s=20.0):
             "cpu_model": cpu_model()}
 
 
+def cpu_single_thread(budget_s=5.0):
+    """The FA prefill slice timing of cpu_baseline on one host thread (the
+    reference harness's cpuCompute is single-threaded): as many (batch,
+    kv-group) slices as fit in about `budget_s` seconds, at least one."""
+    from oracle import oracle as orc
+    prev = orc.get_threads()
+    orc.set_threads(1)
+    try:
+        rng = np.random.default_rng(7)
+        S, D, Hkv, H = FA_S, FA_D, FA_HKV, FA_H
+        nbp = S // 16
+        G = H // Hkv
+        q = orc.from_float(rng.standard_normal((S, H, D), dtype=np.float32), orc.BF16)
+        kc = orc.from_float(rng.standard_normal((nbp, Hkv, 16, D), dtype=np.float32), orc.BF16)
+        vc = orc.from_float(rng.standard_normal((nbp, Hkv, 16, D), dtype=np.float32), orc.BF16)
+        bt = np.arange(nbp, dtype=np.int32)[None]
+        slice_flop = 4 * G * D * S * (S + 1) // 2
+        done, t_total = 0, 0.0
+        while done < FA_B * Hkv:
+            g = done % Hkv
+            t0 = time.perf_counter()
+            orc.flash_attention(q, kc, vc, bt, [S], [S], dtype=orc.BF16, b_only=0,
+                                h_begin=g * G, h_end=(g + 1) * G)
+            t_total += time.perf_counter() - t0
+            done += 1
+            if t_total >= budget_s:
+                break
+    finally:
+        orc.set_threads(prev)
+    return {"value": done * slice_flop / t_total / 1e12, "unit": "TFLOP/s", "cores": 1,
+            "sample": f"{done} (batch, kv-group) slice(s) of the prefill config in {t_total:.2f} s"}
+
+
+def cpu_ops(threads):
+    """Times the CPU oracle on every other op at its full BASELINE config
+    (median of 3 runs; FA decode once), on `threads` host threads.  A
+    reported baseline beside the GPU figures, not a target."""
+    from oracle import oracle as orc
+    if threads > 0:
+        orc.set_threads(threads)
+    used = orc.get_threads()
+    rng = np.random.default_rng(11)
+
+    # Inputs repeat a 1 Mi-element pool of seeded values, uniform on (-1, 1)
+    # (the oracle's time does not depend on the values); this keeps the
+    # set-up of the 270 M-element decode caches to a copy.
+    pool = rng.random(1 << 20, dtype=np.float32) * 2.0 - 1.0
+    pools = {orc.HALF: orc.from_float(pool, orc.HALF), orc.BF16: orc.from_float(pool, orc.BF16)}
+
+    def bits(shape, scale=1.0, dt=None):
+        dt = dt if dt is not None else orc.HALF
+        if scale == 1.0:
+            return np.resize(pools[dt], shape)
+        return orc.from_float(np.resize(pool, shape) * np.float32(scale), dt)
+
+    def timed(fn, runs=3):
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return 1e3 * sorted(ts)[len(ts) // 2]
+
+    res = {}
+    x = bits((4096, 4096))
+    w = orc.from_float(rng.uniform(0.5, 1.5, 4096).astype(np.float32))
+    res["rms_norm"] = timed(lambda: orc.rms_norm(x, w, eps=1e-6))
+    T, Hkv, D, NB, BS = 8192, 8, 128, 1024, 16
+    key, val = bits((T, Hkv, D)), bits((T, Hkv, D))
+    slots = rng.permutation(NB * BS)[:T].astype(np.int64)
+    kc = np.zeros((NB, Hkv, BS, D), np.uint16)
+    vc = np.zeros_like(kc)
+    res["reshape_and_cache"] = timed(lambda: orc.reshape_and_cache(key, val, slots, kc, vc))
+    cx = bits((8, 4096, 2048))
+    cw, cb = bits((4096, 4), 0.5), bits((4096,))
+    cst = np.zeros((8, 3, 4096), np.uint16)
+    res["causal_conv1d"] = timed(lambda: orc.causal_conv1d(cx, cw, bias=cb, conv_state=cst))
+    q, k = bits((8192, 32, 128)), bits((8192, 8, 128))
+    pos = (np.arange(8192) % 2048).astype(np.int64)
+    res["rotary"] = timed(lambda: orc.rotary_embedding(pos, q, k))
+    N, K = 14336, 4096
+    W = bits((N, K), 0.02)
+    Wq = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    sc = orc.from_float(rng.uniform(0.001, 0.01, N).astype(np.float32))
+    for b in (1, 8):
+        xv = bits((b, K))
+        res[f"gemv_f16_b{b}"] = timed(lambda: orc.gemv(W, xv))
+        res[f"gemv_i8_b{b}"] = timed(lambda: orc.gemv_int8(Wq, sc, xv))
+    # decode: the bench's lengths (seed 1008), contiguous blocks
+    lens = np.random.default_rng(1008).integers(512, 8193, 64)
+    nblk = (lens + 15) // 16
+    bt = np.zeros((64, 512), np.int32)
+    off = np.concatenate([[0], np.cumsum(nblk)])
+    for b in range(64):
+        bt[b, :nblk[b]] = np.arange(off[b], off[b + 1])
+    dk = bits((int(off[-1]), FA_HKV, 16, FA_D), dt=orc.BF16)
+    dv = bits((int(off[-1]), FA_HKV, 16, FA_D), dt=orc.BF16)
+    dq = bits((64, FA_H, FA_D), dt=orc.BF16)
+    res["fa_decode"] = timed(lambda: orc.flash_attention(dq, dk, dv, bt, np.ones(64, np.int32),
+                                                         lens.astype(np.int32), dtype=orc.BF16),
+                             runs=1)
+    return {"cores": used, "unit": "ms", "kind": "port",
+            "sample": "full BASELINE config of each op (median of 3 runs; fa_decode 1 run)",
+            "ms": {k: round(v, 3) for k, v in res.items()}}
+
+
 def cpu_model():
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
@@ -388,6 +496,8 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_threads)
+        line["cpu_baseline"]["single_thread"] = cpu_single_thread()
+        line["cpu_ops"] = cpu_ops(args.cpu_threads)
     print(json.dumps(line), flush=True)
 
 

@@ -117,6 +117,67 @@ def test_decode_many_splits_combine_fallback():
         check(case, orc.BF16, seed=H)
 
 
+def run_gpu_workspace(q, kc, vc, bt, q_lens, kv_lens, dtype, fill):
+    """tecoopsFlashAttentionEx with a caller workspace (filled with byte
+    `fill` first): the split partials go there and the separate merge kernel
+    combines them."""
+    import ctypes
+    from tecoops import _lib
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    tdt = torch.float16 if dtype == orc.HALF else torch.bfloat16
+    code = _lib.DATA_HALF if dtype == orc.HALF else _lib.DATA_BFLOAT16
+    out = torch.empty(q.shape, dtype=tdt, device="cuda")
+    H, D = q.shape[1], q.shape[2]
+    need = ctypes.c_size_t()
+    _lib.call("tecoopsGetFlashAttentionWorkspaceSize", len(q_lens), H, D, max(q_lens),
+              max(kv_lens), ctypes.byref(need))
+    ws = torch.full((need.value,), fill, dtype=torch.uint8, device="cuda")
+    q_d, k_d, v_d, bt_d = dev(q, dtype), dev(kc, dtype), dev(vc, dtype), dev(bt)
+    cu_d, kl_d = dev(cu), dev(np.array(kv_lens, np.int32))
+    with tecoops._Desc(bt_d, _lib.DATA_INT32) as btd, tecoops._Desc(q_d, code) as qd, \
+            tecoops._Desc(k_d, code) as kd, tecoops._Desc(v_d, code) as vd, \
+            tecoops._Desc(out, code) as od:
+        _lib.call("tecoopsFlashAttentionEx", tecoops._handle(out.device), max(q_lens),
+                  max(kv_lens), None, ctypes.c_void_p(cu_d.data_ptr()),
+                  ctypes.c_void_p(kl_d.data_ptr()), btd, ctypes.c_void_p(bt_d.data_ptr()), qd,
+                  ctypes.c_void_p(q_d.data_ptr()), kd, ctypes.c_void_p(k_d.data_ptr()), vd,
+                  ctypes.c_void_p(v_d.data_ptr()), od, ctypes.c_void_p(out.data_ptr()),
+                  ctypes.c_float(1.0 / math.sqrt(D)), 1, ctypes.c_void_p(ws.data_ptr()))
+    torch.cuda.synchronize()
+    return as_f32(out, dtype)
+
+
+def test_decode_caller_workspace():
+    """A caller workspace (any prior contents) holds the split partials:
+    short and long contexts, the merge kernel's LDS-staged path and (128
+    splits x 32 columns) its two-pass path."""
+    for H, Hkv, kv, fill in ((32, 8, [1, 17, 600, 2049, 3000], 0xFF), (32, 1, [16384], 0x7F),
+                             (8, 2, [16384], 0x00)):
+        q_lens = [1] * len(kv)
+        q, kc, vc, bt = make_inputs(40 + H + Hkv, H, Hkv, 128, 16, q_lens, kv, dtype=orc.BF16)
+        got = run_gpu_workspace(q, kc, vc, bt, q_lens, kv, orc.BF16, fill)
+        ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=orc.BF16)
+        assert_close(got, ref, what=f"workspace {H}/{Hkv} {kv}")
+
+
+def test_decode_launches_in_a_row_share_scratch():
+    """Decode launches in a row on one handle reuse (and grow) its split-KV
+    scratch: different batch shapes and split counts (1 to 157 splits per
+    sequence) all match the oracle, twice over."""
+    r = np.random.default_rng(77)
+    shapes = [(32, 8, r.integers(512, 8193, 64).tolist()),
+              (32, 8, [9000, 1, 2048, 2049, 7000]),
+              (16, 2, [20000, 5]),
+              (32, 8, r.integers(512, 8193, 64).tolist())]
+    for rep in range(2):
+        for i, (H, Hkv, kv) in enumerate(shapes):
+            q_lens = [1] * len(kv)
+            q, kc, vc, bt = make_inputs(60 + i, H, Hkv, 128, 16, q_lens, kv, dtype=orc.BF16)
+            got = run_gpu(q, kc, vc, bt, q_lens, kv, orc.BF16)
+            ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=orc.BF16)
+            assert_close(got, ref, what=f"rep {rep} shape {i}")
+
+
 def test_softmax_scale_honoured():
     q, kc, vc, bt = make_inputs(6, 4, 2, 64, 16, [10], [30])
     got = run_gpu(q, kc, vc, bt, [10], [30], scale=0.3)
