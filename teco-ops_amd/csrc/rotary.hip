@@ -25,6 +25,16 @@ constexpr int kMaxHalf = 256;  // rot_dim <= 512
 
 constexpr int kTokensPerBlock = 4;
 
+// o1 = x1 cos - x2 sin, o2 = x2 cos + x1 sin with the roundings spelled out
+// (one product, then one fused multiply-add), so every kernel that rotates
+// gets bit-identical results whatever the compiler would contract.
+__device__ __forceinline__ float rot1(float x1, float x2, float c, float s) {
+    return fmaf(x1, c, -(x2 * s));
+}
+__device__ __forceinline__ float rot2(float x1, float x2, float c, float s) {
+    return fmaf(x2, c, x1 * s);
+}
+
 // Rotation of 4 NeoX pairs (x1 = a, x2 = b, 4 elements each, as 8-byte words)
 // with (cos, sin) c[0..3]: o1 = x1 cos - x2 sin, o2 = x2 cos + x1 sin.
 template <typename T>
@@ -37,8 +47,8 @@ __device__ __forceinline__ void rot_neox4(const uint2 &a, const uint2 &b, const 
         const float2 c0 = c[2 * w], c1 = c[2 * w + 1];
         const float x10 = lo<T>(pa[w]), x11 = hi<T>(pa[w]);
         const float x20 = lo<T>(pb[w]), x21 = hi<T>(pb[w]);
-        qa[w] = pack<T>(x10 * c0.x - x20 * c0.y, x11 * c1.x - x21 * c1.y);
-        qb[w] = pack<T>(x20 * c0.x + x10 * c0.y, x21 * c1.x + x11 * c1.y);
+        qa[w] = pack<T>(rot1(x10, x20, c0.x, c0.y), rot1(x11, x21, c1.x, c1.y));
+        qb[w] = pack<T>(rot2(x10, x20, c0.x, c0.y), rot2(x11, x21, c1.x, c1.y));
     }
     oa = make_uint2(qa[0], qa[1]);
     ob = make_uint2(qb[0], qb[1]);
@@ -63,7 +73,7 @@ __device__ __forceinline__ uint4 rot_gptj4(const uint4 &a, const float2 *c) {
     for (int w = 0; w < 4; ++w) {
         const float2 cc = c[w];
         const float x1 = lo<T>(pa[w]), x2 = hi<T>(pa[w]);
-        pa[w] = pack<T>(x1 * cc.x - x2 * cc.y, x2 * cc.x + x1 * cc.y);
+        pa[w] = pack<T>(rot1(x1, x2, cc.x, cc.y), rot2(x1, x2, cc.x, cc.y));
     }
     return make_uint4(pa[0], pa[1], pa[2], pa[3]);
 }
@@ -73,8 +83,8 @@ template <typename T>
 __device__ __forceinline__ void rot_pair(uint16_t x1b, uint16_t x2b, float2 cc, uint16_t &o1,
                                          uint16_t &o2) {
     const float x1 = Cvt<T>::to(x1b), x2 = Cvt<T>::to(x2b);
-    o1 = Cvt<T>::from(x1 * cc.x - x2 * cc.y);
-    o2 = Cvt<T>::from(x2 * cc.x + x1 * cc.y);
+    o1 = Cvt<T>::from(rot1(x1, x2, cc.x, cc.y));
+    o2 = Cvt<T>::from(rot2(x1, x2, cc.x, cc.y));
 }
 
 // VW: 0 one pair per task; 1 four pairs (8-byte NeoX / 16-byte GPT-J words);

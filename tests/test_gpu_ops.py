@@ -146,6 +146,39 @@ def test_rotary_variants(is_neox, use_cache):
     _run_rotary(300, 4, 2, 128, seed=5, is_neox=is_neox, use_cache=use_cache)
 
 
+def test_rotary_wide_heads_tails_and_skips():
+    """NeoX 16-byte path: 72 heads x 16 tasks per token (rot_dim 256) make
+    several task rounds per thread; 303 tokens leave a partial last
+    workgroup; with the cos/sin cache, positions past it are left
+    unrotated; without a key only q rotates; rot_dim < head_size leaves the
+    tail untouched."""
+    r = rng(31)
+    T, H, Hkv, D = 303, 64, 8, 256
+    q = bits(r.standard_normal((T, H, D)))
+    k = bits(r.standard_normal((T, Hkv, D)))
+    pos = r.integers(0, 1100, T).astype(np.int64)
+    i = np.arange(D // 2)
+    th = np.arange(1000)[:, None] * 10000.0 ** (-2 * i / D)
+    cache = np.concatenate([np.cos(th), np.sin(th)], 1).astype(np.float32)
+    qo, ko = orc.rotary_embedding(pos, q, k, cos_sin_cache=cache)
+    qt, kt = dev(q), dev(k)
+    tecoops.rotary_embedding(dev(pos), qt, kt, D, dev(cache))
+    torch.cuda.synchronize()
+    assert_close(as_f32(qt), qo, what="rotary q, cache")
+    assert_close(as_f32(kt), ko, what="rotary k, cache")
+    skipped = pos >= 1000
+    assert skipped.any() and np.array_equal(host_bits(qt)[skipped], q[skipped])
+    # no key, rot_dim 64 of head_size 128
+    q2 = bits(r.standard_normal((T, 8, 128)))
+    pos2 = (np.arange(T) % 2048).astype(np.int64)
+    qo2, _ = orc.rotary_embedding(pos2, q2, None, rot_dim=64)
+    qt2 = dev(q2)
+    tecoops.rotary_embedding(dev(pos2), qt2, None, 128, rot_dim=64)
+    torch.cuda.synchronize()
+    assert_close(as_f32(qt2), qo2, what="rotary q only, rot_dim 64")
+    assert np.array_equal(host_bits(qt2)[:, :, 64:], q2[:, :, 64:])
+
+
 def test_rotary_partial_rot_dim_bf16_and_scalar_path():
     _run_rotary(64, 3, 1, 64, seed=6, rot_dim=32, dtype=orc.BF16)
     _run_rotary(64, 3, 1, 20, seed=7, rot_dim=10)   # rot/2 = 5: scalar path
