@@ -20,7 +20,8 @@ this steady state an op's HBM traffic per launch equals its algorithmic bytes
 (its own dirty outputs are written back during later launches).  Per-op kernel
 time: K back-to-back launches of the op between one pair of torch.cuda events
 on the stream the ops are enqueued on (tecoops binds the current torch
-stream), divided by K.
+stream), divided by K, right after a warm-up of at least W launches and 30 ms
+of the same op.
 
 Prints ONE JSON line.  `value` is flash-attention prefill TFLOP/s (causal
 FLOP count / average kernel time), the throughput figure of BASELINE.json's
@@ -81,6 +82,7 @@ def seeded_bits(rng, shape, kind="normal", scale=1.0, lo=0.0, hi=1.0, dtype="f16
 
 
 ROTATE_BYTES = 1 << 30   # rotating working set per op: 4x the 256 MiB MALL
+WARM_S = 0.03            # minimum warm-up per op, seconds of its own launches
 
 
 def copies_for(ws_bytes, limit=16):
@@ -420,25 +422,31 @@ def main():
     ops = build_ops(keep)
     if keep:
         ops = {k: v for k, v in ops.items() if k in keep}
-    # Warm-up, then the timed region: K steps, a step being one launch of
-    # every op.  Launches of one op run back to back (rotating over its input
-    # copies) between one pair of events on the stream they are enqueued on,
-    # so the average per launch excludes host overhead.
-    for fns, _ in ops.values():
-        for i in range(args.warmup):
-            fns[i % len(fns)]()
-    torch.cuda.synchronize()
+    # Per op: warm-up, then the timed region of K launches.  The warm-up runs
+    # at least W launches and at least WARM_S seconds of the op's own work
+    # right before its timed region, so the GPU clock has settled under that
+    # load (a cold start measured FA prefill 13 % slow).  Launches of one op
+    # run back to back (rotating over its input copies) between one pair of
+    # events on the stream they are enqueued on, so the average per launch
+    # excludes host overhead.
     ev = {}
-    t0 = time.perf_counter()
+    wall = 0.0
     for n, (fns, _) in ops.items():
+        i, t_w = 0, time.perf_counter()
+        while i < args.warmup or time.perf_counter() - t_w < WARM_S:
+            for _ in range(max(1, min(args.warmup, 10))):
+                fns[i % len(fns)]()
+                i += 1
+            torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
         a.record()
         for i in range(args.steps):
             fns[i % len(fns)]()
         b.record()
+        torch.cuda.synchronize()
+        wall += time.perf_counter() - t0
         ev[n] = (a, b)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
 
     report = {}
     for n, (fns, work) in ops.items():
