@@ -434,15 +434,20 @@ def main():
     for n, (fns, _) in ops.items():
         i, t_w = 0, time.perf_counter()
         while i < args.warmup or time.perf_counter() - t_w < WARM_S:
-            for _ in range(max(1, min(args.warmup, 10))):
+            for _ in range(10):
                 fns[i % len(fns)]()
                 i += 1
             torch.cuda.synchronize()
+        # ten more warm-up launches left in flight: the timed launches queue
+        # behind them, so the GPU never waits for the host between the two
+        for _ in range(10):
+            fns[i % len(fns)]()
+            i += 1
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         a.record()
-        for i in range(args.steps):
-            fns[i % len(fns)]()
+        for j in range(args.steps):  # the rotation continues where the warm-up left it
+            fns[(i + j) % len(fns)]()
         b.record()
         torch.cuda.synchronize()
         wall += time.perf_counter() - t0
