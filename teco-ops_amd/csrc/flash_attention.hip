@@ -857,27 +857,6 @@ bool reserve_lds(const void *kernel, size_t bytes) {
     return true;
 }
 
-// Prefill shape: W waves per workgroup and TILE keys per K/V tile.
-struct PrefillCfg {
-    int w, tile;
-};
-
-// Prefill variant for D = 128 with the uniform-page loader: 12 waves (3 per
-// SIMD) and 96-key tiles by default; TECOOPS_FA_PREFILL="8,1,64" selects the
-// 8-wave, 64-key-tile variant (A/B measurements).
-PrefillCfg prefill_cfg() {
-    static PrefillCfg cfg = [] {
-        PrefillCfg c{12, 96};
-        if (const char *e = std::getenv("TECOOPS_FA_PREFILL")) {
-            int w = 0, q = 0, t = 0;
-            if (std::sscanf(e, "%d,%d,%d", &w, &q, &t) == 3 && w == 8 && q == 1 && t == 64)
-                c = PrefillCfg{8, 64};
-        }
-        return c;
-    }();
-    return cfg;
-}
-
 template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
 tecoopsStatus_t launch_prefill(const FaParams &p, int max_q, hipStream_t s) {
     constexpr int QT = 32 * QSUB * (W / HW);
@@ -918,8 +897,7 @@ tecoopsStatus_t run(tecoopsHandle_t handle, FaParams &p, const Plan &pl, int max
         return pow2 ? prefill_hw<T, D, 4, 1, true>(p, max_q, s)
                     : prefill_hw<T, D, 4, 1, false>(p, max_q, s);
     }
-    const PrefillCfg c = prefill_cfg();
-    if (c.w == 8) return prefill_hw<T, D, 8, 1, true, 64>(p, max_q, s);
+    // D = 128 with the uniform-page loader: 12 waves (3 per SIMD), 96-key tiles
     return prefill_hw<T, D, 12, 1, true, 96>(p, max_q, s);
 }
 
