@@ -12,6 +12,7 @@
 
 #include <cstdio>
 #include <cstdint>
+#include <atomic>
 #include <cstring>
 
 #include "tecoops.h"
@@ -75,6 +76,22 @@ __host__ __device__ inline bool aligned(const void *p, size_t a) {
 
 inline unsigned ceil_div(long long a, long long b) {
     return static_cast<unsigned>((a + b - 1) / b);
+}
+
+// Compute units of the current device, queried once per device (256 on
+// MI355X; 256 is also the answer when the query fails).
+inline int device_cus() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            v <= 0)
+            v = 256;
+        cached[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
 }
 
 // Returns a device buffer of at least `bytes` owned by the handle.  Growing

@@ -101,18 +101,56 @@ __device__ __forceinline__ float half_swap_sum(float x) {
            __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
 }
 
+// Lane l combined with the lane that dpp_ctrl CTRL selects within its row of
+// 16 (a DPP operand of the VALU op, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane 7 - l within each 8 lanes
+constexpr int kDppMirror = 0x140;      // lane 15 - l within each 16 lanes
+constexpr int kDppRor4 = 0x124;        // rotation by 4 lanes within each 16
+constexpr int kDppRor8 = 0x128;        // rotation by 8 lanes within each 16
+
+// Rows 2i and 2i + 1 (16 lanes each) combined through v_permlane16_swap: with
+// both operands equal to x, the two results hold row 2i and row 2i + 1 of x in
+// both rows of the pair.
+__device__ __forceinline__ float row_swap_sum(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) +
+           __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+__device__ __forceinline__ float row_swap_max(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(r[0])),
+                 __builtin_bit_cast(float, static_cast<uint32_t>(r[1])));
+}
+
+// Sum over the 64 lanes, in every lane, without LDS: pairs, quads, halves and
+// rows through DPP, then row pairs and wave halves through the permlane swaps.
+// Every step adds two operands that the partner lane adds too, so all lanes
+// end with the same bits.
 __device__ __forceinline__ float wave_sum(float v) {
-    v = half_swap_sum(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
+    v = row_swap_sum(v);
+    return half_swap_sum(v);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-    v = half_swap_max(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppMirror>(v));
+    v = row_swap_max(v);
+    return half_swap_max(v);
 }
 
 }  // namespace dev

@@ -14,14 +14,17 @@
 //     matrix-core path ("MFMA path" below), in slices of 16 columns.
 //   * 1-2 and all other shapes: the VALU path, which streams W fastest when
 //     there is little math per byte.  A workgroup of 4 waves owns 4*R
-//     consecutive output rows and first stages x ([B, K], at most 64 KiB) in
-//     LDS.  Each wave streams R rows of W with 16-byte loads, lane-interleaved
+//     consecutive output rows and stages x ([B, K], at most 64 KiB) in
+//     LDS; x (and the int8 scales) are loaded before W, so that waiting for
+//     them leaves W in flight.  Each wave streams R rows of W with 16-byte
+//     loads, lane-interleaved
 //     along K so that every load instruction reads a contiguous 1 KiB run of
 //     a row; a lane issues the loads of CPL chunks of each row before using
 //     any (a whole fp16 row, or two int8 rows, in flight per wave at K =
 //     4096), and keeps R x B fp32 partial sums; the products use
 //     v_dot2_f32_{f16,bf16} (two MACs per instruction, fp32 accumulation).  A
-//     wave-wide xor-shuffle reduction finishes each (row, batch) sum.
+//     wave reduction through DPP and permlane swaps (wave_sum, no LDS)
+//     finishes each (row, batch) sum.
 // int8 weights are widened exactly to fp16 with one v_perm_b32 (bytes of
 // w+128 under the exponent of 1024.0) and one packed fp16 subtract of 1152 per
 // weight pair; the per-row int8 scale is applied to the fp32 sum.
@@ -59,11 +62,38 @@ __device__ __forceinline__ uint4 load_stream(const uint4 *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Copies x [B, K] (16-bit elements, K % 8 == 0) into LDS.
-__device__ __forceinline__ void stage_x(uint4 *xs, const uint4 *x, int nvec) {
-    for (int i = threadIdx.x; i < nvec; i += blockDim.x) xs[i] = x[i];
+// Copies x [B, K] (16-bit elements, K % 8 == 0, nvec 16-byte chunks) into
+// LDS in two halves.  x_pre loads the first XP chunks of each thread into
+// registers and is called before the W loads, so that waiting for x later
+// leaves the younger W loads in flight (loads complete in order); x_post
+// stores them, copies any remaining chunks and synchronises the workgroup.
+template <int XP>
+__device__ __forceinline__ void x_pre(uint4 (&xr)[XP], const uint4 *x, int nvec) {
+    // Relaxed workgroup-scope atomic loads (plain global loads in the ISA):
+    // the compiler neither sinks them to their use nor hoists the W loads
+    // above them, as it does with ordinary loads of read-only memory.
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+        const uint64_t *p = reinterpret_cast<const uint64_t *>(
+            x + min(static_cast<int>(threadIdx.x + j * blockDim.x), nvec - 1));
+        const uint64_t lo = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const uint64_t hi = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        xr[j] = make_uint4(static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32),
+                           static_cast<uint32_t>(hi), static_cast<uint32_t>(hi >> 32));
+    }
+}
+template <int XP>
+__device__ __forceinline__ void x_post(uint4 *xs, const uint4 (&xr)[XP], const uint4 *x, int nvec) {
+    // unconditional (clamped) stores: a store under a branch lets the
+    // compiler sink its load into that branch, behind the W loads; threads
+    // past the end all write x's last chunk to its own place
+#pragma unroll
+    for (int j = 0; j < XP; ++j) xs[min(static_cast<int>(threadIdx.x + j * blockDim.x), nvec - 1)] = xr[j];
+    for (int i = threadIdx.x + XP * blockDim.x; i < nvec; i += blockDim.x) xs[i] = x[i];
     __syncthreads();
 }
+// x chunks per thread loaded ahead of W: all of x for B = 1 and K <= 4096.
+constexpr int x_pre_chunks(int B) { return B == 1 ? 2 : 4; }
 
 // int8 weight dword (4 values) -> two packed fp16 pairs holding the exact values.
 __device__ __forceinline__ void widen_i8(uint32_t w, uint32_t &p01, uint32_t &p23) {
@@ -92,13 +122,21 @@ gemv_i8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
     const uint4 *wrow[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kw;
+    // the scales and x are loaded before W: they are waited for without
+    // draining the W loads, and the scales are in registers by the end
+    uint16_t sc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) sc[r] = scales[min(n0 + r, N - 1)];
+    uint4 xr[x_pre_chunks(B)];
+    x_pre(xr, x, B * kx);
+    // W loads are unconditional (clamped to the row's last chunk) so that the
+    // compiler waits for each one at its use rather than for all of them
     uint4 q[R][CPL];
 #pragma unroll
     for (int u = 0; u < CPL; ++u)
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            q[r][u] = lane + 64 * u < kw ? load_stream(wrow[r] + lane + 64 * u) : uint4{};
-    stage_x(xs, x, B * kx);
+        for (int r = 0; r < R; ++r) q[r][u] = load_stream(wrow[r] + min(lane + 64 * u, kw - 1));
+    x_post(xs, xr, x, B * kx);
     if (n0 >= N) return;
     float acc[R][B];
 #pragma unroll
@@ -135,16 +173,15 @@ gemv_i8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
 #pragma unroll
         for (int u = 0; u < CPL; ++u)
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (cn + 64 * u < kw) q[r][u] = load_stream(wrow[r] + cn + 64 * u);
+            for (int r = 0; r < R; ++r) q[r][u] = load_stream(wrow[r] + min(cn + 64 * u, kw - 1));
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const float sc = (n0 + r < N) ? h2f(scales[n0 + r]) : 0.0f;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const float s = wave_sum(acc[r][b]);
-            if (lane == 0 && n0 + r < N) y[static_cast<long long>(b) * N + n0 + r] = f2h(sc * s);
+            if (lane == 0 && n0 + r < N)
+                y[static_cast<long long>(b) * N + n0 + r] = f2h(h2f(sc[r]) * s);
         }
     }
 }
@@ -161,13 +198,14 @@ gemv16_kernel(const uint4 *__restrict__ W, const uint4 *__restrict__ x,
     const uint4 *wrow[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<long long>(min(n0 + r, N - 1)) * kv;
+    uint4 xr[x_pre_chunks(B)];
+    x_pre(xr, x, B * kv);
     uint4 q[R][CPL];
 #pragma unroll
     for (int u = 0; u < CPL; ++u)
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            q[r][u] = lane + 64 * u < kv ? load_stream(wrow[r] + lane + 64 * u) : uint4{};
-    stage_x(xs, x, B * kv);
+        for (int r = 0; r < R; ++r) q[r][u] = load_stream(wrow[r] + min(lane + 64 * u, kv - 1));
+    x_post(xs, xr, x, B * kv);
     if (n0 >= N) return;
     float acc[R][B];
 #pragma unroll
@@ -199,8 +237,7 @@ gemv16_kernel(const uint4 *__restrict__ W, const uint4 *__restrict__ x,
 #pragma unroll
         for (int u = 0; u < CPL; ++u)
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (cn + 64 * u < kv) q[r][u] = load_stream(wrow[r] + cn + 64 * u);
+            for (int r = 0; r < R; ++r) q[r][u] = load_stream(wrow[r] + min(cn + 64 * u, kv - 1));
     }
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -431,9 +468,10 @@ gemv_i8_mfma_kernel(const int8_t *__restrict__ W, const uint16_t *__restrict__ s
 // (256-byte) run of row n0 + r, so one load instruction reads four contiguous
 // 256-byte row segments (the access pattern of the VALU path), and block blk
 // accumulates those 4 rows against batch columns 4*cg + r over its own k
-// values.  The 16 blocks hold partial sums over disjoint k; a butterfly over
-// lanes l ^ 4, ^ 8, ^ 16, ^ 32 adds them once the wave has covered K.  No
-// cross-wave reduction or barrier follows the staging of x.
+// values.  The 16 blocks hold partial sums over disjoint k; once the wave has
+// covered K they are added across lanes l, l + 4, ..., l + 60 without LDS
+// (DPP row rotations by 4 and 8, then the row-pair and half-wave permlane
+// swaps).  No cross-wave reduction or barrier follows the staging of x.
 //   x is staged in LDS as [4*NCG][K] 16-bit values with the 16-byte chunks of
 //   row i XOR-swizzled by 4*(i % 4) inside each 256-byte run, so that the
 //   128-bit B-operand reads of lanes 0-7 (rows 0-3, two chunks) hit distinct
@@ -494,9 +532,17 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
     for (int g = 0; g < RG; ++g)
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg) acc[g][cg] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    // The x loads are issued first (unconditionally, clamped to the last
-    // chunk), so that waiting for them leaves the younger W loads in flight.
-    constexpr int XPT = kMaxXChunks / (NW * 64);  // x chunks per thread
+    // The scales (int8) and x loads are issued first (unconditionally,
+    // clamped to the last row / chunk), so that waiting for x leaves the
+    // younger W loads in flight and the scales are in registers by the end.
+    uint16_t sc[RG][4];
+    if constexpr (I8) {
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sc[g][v] = scales[min(n0 + 4 * g + v, N - 1)];
+    }
+    constexpr int XPT = (kMaxXChunks + NW * 64 - 1) / (NW * 64);  // x chunks per thread
     const int nxc = NCG * 4 * kx;
     uint4 xr[XPT];
 #pragma unroll
@@ -505,6 +551,12 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
         const int row = min(idx / kx, B - 1);
         xr[j] = x[static_cast<long long>(row) * kx + idx % kx];
     }
+    // This lane's x chunks in LDS: chunk 16i + blk (fp16 W) or 32i + 2blk and
+    // the next (int8 W) of row 4cg + r.  The swizzle xor (4r < 16) stays below
+    // the step's bits, so xs_chunk(4cg + r, c0 + 16i, K) = xs_chunk(4cg + r,
+    // c0, K) + 128i (c0 = blk), likewise with 32i (c0 = 2blk), and rows 4
+    // apart keep the same xor: one base address per lane.
+    const uint16_t *xs_lane = xs + xs_chunk(r, I8 ? 2 * blk : blk, K);
     uint4 q[CPL][RG];
     // Each wave starts its sweep of K at a different load step, so that the
     // requests in flight across the grid spread over all HBM channels instead
@@ -533,11 +585,10 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
                 }
 #pragma unroll
                 for (int cg = 0; cg < NCG; ++cg) {
-                    const int row = 4 * cg + r;
-                    const uint4 xa = *reinterpret_cast<const uint4 *>(
-                        xs + xs_chunk(row, 32 * i + 2 * blk, K));
-                    const uint4 xb = *reinterpret_cast<const uint4 *>(
-                        xs + xs_chunk(row, 32 * i + 2 * blk + 1, K));
+                    // chunks 32i + 2blk and 32i + 2blk + 1 of row 4cg + r
+                    const uint4 *xp = reinterpret_cast<const uint4 *>(xs_lane + cg * 4 * K) + 32 * i;
+                    const uint4 xa = xp[0];
+                    const uint4 xb = xp[1];
 #pragma unroll
                     for (int g = 0; g < RG; ++g) {
                         f32x4_t c = acc[g][cg];
@@ -551,8 +602,8 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
             } else {
 #pragma unroll
                 for (int cg = 0; cg < NCG; ++cg) {
-                    const uint4 xv = *reinterpret_cast<const uint4 *>(
-                        xs + xs_chunk(4 * cg + r, 16 * i + blk, K));
+                    // chunk 16i + blk of row 4cg + r
+                    const uint4 xv = reinterpret_cast<const uint4 *>(xs_lane + cg * 4 * K)[16 * i];
 #pragma unroll
                     for (int g = 0; g < RG; ++g) {
                         acc[g][cg] = Mma4<T>::run(q[u][g].x, q[u][g].y, xv.x, xv.y, acc[g][cg]);
@@ -575,8 +626,9 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
             __syncthreads();
         });
     if (n0 >= N) return;
-    // add the 16 blocks' partial sums; lanes 0-3 then hold column r of rows
-    // n0 + 4g .. n0 + 4g + 3
+    // add the 16 blocks' partial sums (lanes r, r + 4, ..., r + 60: rotations
+    // by 4 and 8 within each row of 16 lanes, then the row-pair and half-wave
+    // swaps); lanes 0-3 then hold column r of rows n0 + 4g .. n0 + 4g + 3
 #pragma unroll
     for (int g = 0; g < RG; ++g)
 #pragma unroll
@@ -584,11 +636,10 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 float t = acc[g][cg][v];
-                t += __shfl_xor(t, 4, 64);
-                t += __shfl_xor(t, 8, 64);
-                t += __shfl_xor(t, 16, 64);
-                t += __shfl_xor(t, 32, 64);
-                acc[g][cg][v] = t;
+                t += dpp<kDppRor4>(t);
+                t += dpp<kDppRor8>(t);
+                t = row_swap_sum(t);
+                acc[g][cg][v] = half_swap_sum(t);
             }
     if (blk == 0) {
 #pragma unroll
@@ -601,7 +652,7 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
                     for (int v = 0; v < 4; ++v) {
                         const int n = n0 + 4 * g + v;
                         if (n < N) {
-                            const float o = I8 ? acc[g][cg][v] * h2f(scales[n]) : acc[g][cg][v];
+                            const float o = I8 ? acc[g][cg][v] * h2f(sc[g][v]) : acc[g][cg][v];
                             y[static_cast<long long>(b) * N + n] = Cvt<T>::from(o);
                         }
                     }
@@ -653,10 +704,10 @@ constexpr int kMfmaMinBatchI8 = 2, kMfmaRTI8 = 4, kMfmaWavesI8 = 8;
 constexpr int kR16 = 1, kCpl16 = 8;
 constexpr int kRI8 = 2, kCplI8 = 4;
 
-// 4x4x4 path: waves per workgroup (x is staged once per workgroup), groups
-// of 4 rows per wave and load steps in flight per lane, for fp16 / int8 W.
-// x fills at most 64 KiB of LDS.
-constexpr int kB8Waves = 16, kB8RgF16 = 1, kB8CplF16 = 8, kB8RgI8 = 1, kB8CplI8 = 4;
+// 4x4x4 path: groups of 4 rows per wave and load steps in flight per lane,
+// for fp16 / int8 W.  x fills at most 64 KiB of LDS and is staged once per
+// workgroup, so workgroups are large (b8_waves picks their size).
+constexpr int kB8RgF16 = 1, kB8CplF16 = 8, kB8RgI8 = 1, kB8CplI8 = 4;
 constexpr int kB8MaxBatch = 8;
 
 bool b8_fits(int batch, int k, bool i8) {
@@ -664,22 +715,55 @@ bool b8_fits(int batch, int k, bool i8) {
     return static_cast<long long>(batch <= 4 ? 4 : 8) * k * 2 <= kMaxLdsBytes;
 }
 
+// Waves per workgroup of the 4x4x4 path: of 16, 14, 12, 8 and 7, the one that
+// leaves the busiest CU the fewest waves (ceil(workgroups / CUs) * waves; the
+// first listed on ties), so that a grid just short of the CU count does not
+// idle CUs: N = 14336 takes 14 waves and 256 workgroups (16 waves: 224).
+int b8_waves(int N, int rows_per_wave) {
+    const long long cus = tecoops::device_cus();
+    int best = 16;
+    long long best_load = -1;
+    for (int nw : {16, 14, 12, 8, 7}) {
+        const long long wgs = tecoops::ceil_div(N, static_cast<long long>(rows_per_wave) * nw);
+        const long long load = (wgs + cus - 1) / cus * nw;
+        if (best_load < 0 || load < best_load) {
+            best_load = load;
+            best = nw;
+        }
+    }
+    return best;
+}
+
+template <typename T, bool I8, int NCG, int NW>
+void launch_b8_nw(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
+                  hipStream_t s) {
+    constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
+    constexpr int CPL = I8 ? kB8CplI8 : kB8CplF16;
+    hipLaunchKernelGGL((gemv_b8_kernel<T, I8, NCG, RG, NW, CPL>),
+                       dim3(tecoops::ceil_div(N, 4 * RG * NW)), dim3(NW * 64), 4 * NCG * K * 2, s,
+                       static_cast<const uint4 *>(W), static_cast<const uint16_t *>(sc),
+                       static_cast<const uint4 *>(x), static_cast<uint16_t *>(y), N, K, B);
+}
+
+template <typename T, bool I8, int NCG>
+void launch_b8_ncg(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
+                   hipStream_t s) {
+    switch (b8_waves(N, 4 * (I8 ? kB8RgI8 : kB8RgF16))) {
+        case 14: launch_b8_nw<T, I8, NCG, 14>(W, sc, x, y, B, N, K, s); break;
+        case 12: launch_b8_nw<T, I8, NCG, 12>(W, sc, x, y, B, N, K, s); break;
+        case 8: launch_b8_nw<T, I8, NCG, 8>(W, sc, x, y, B, N, K, s); break;
+        case 7: launch_b8_nw<T, I8, NCG, 7>(W, sc, x, y, B, N, K, s); break;
+        default: launch_b8_nw<T, I8, NCG, 16>(W, sc, x, y, B, N, K, s); break;
+    }
+}
+
 template <typename T, bool I8>
 void launch_b8(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                hipStream_t s) {
-    constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
-    constexpr int CPL = I8 ? kB8CplI8 : kB8CplF16;
-    const unsigned grid = tecoops::ceil_div(N, 4 * RG * kB8Waves);
-    const uint4 *w4 = static_cast<const uint4 *>(W);
-    const uint16_t *s16 = static_cast<const uint16_t *>(sc);
-    const uint4 *x4 = static_cast<const uint4 *>(x);
-    uint16_t *y16 = static_cast<uint16_t *>(y);
     if (B <= 4)
-        hipLaunchKernelGGL((gemv_b8_kernel<T, I8, 1, RG, kB8Waves, CPL>), dim3(grid),
-                           dim3(kB8Waves * 64), 4 * K * 2, s, w4, s16, x4, y16, N, K, B);
+        launch_b8_ncg<T, I8, 1>(W, sc, x, y, B, N, K, s);
     else
-        hipLaunchKernelGGL((gemv_b8_kernel<T, I8, 2, RG, kB8Waves, CPL>), dim3(grid),
-                           dim3(kB8Waves * 64), 8 * K * 2, s, w4, s16, x4, y16, N, K, B);
+        launch_b8_ncg<T, I8, 2>(W, sc, x, y, B, N, K, s);
 }
 
 template <typename T, int B>

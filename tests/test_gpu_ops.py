@@ -506,6 +506,32 @@ def test_gemv_int8_small_batch_matrix_core(B, K):
                  what=f"gemv_int8 {B}x{N}x{K}")
 
 
+@pytest.mark.parametrize("N", [16384, 14336, 12288, 301])
+@pytest.mark.parametrize("i8", [False, True])
+def test_gemv_small_batch_workgroup_sizes(N, i8):
+    """The 4x4x4 path sizes its workgroups from N and the CU count: on 256
+    CUs these N take 16, 14, 12 and 8 waves per workgroup (the grid stages x
+    once per workgroup; waves past the last row still stage their share)."""
+    r = rng(950 + N + i8)
+    B, K = 5, 256
+    x = bits(r.standard_normal((B, K)))
+    y = torch.empty((B, N), dtype=torch.float16, device="cuda")
+    if i8:
+        W = r.integers(-127, 128, (N, K), dtype=np.int8)
+        s = bits(r.uniform(0.001, 0.01, N))
+        ref = orc.gemv_int8(W, s, x)
+        tecoops.gemv_int8(dev(W), dev(s), dev(x), y)
+        torch.cuda.synchronize()
+        assert_close(as_f32(y), ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2,
+                     what=f"gemv_int8 {B}x{N}x{K}")
+    else:
+        W = bits(r.normal(0, 0.05, (N, K)))
+        ref = orc.gemv(W, x)
+        tecoops.gemv(dev(W), dev(x), y)
+        torch.cuda.synchronize()
+        assert_close(as_f32(y), ref, what=f"gemv {B}x{N}x{K}")
+
+
 def test_gemv_odd_shapes_and_bf16():
     r = rng(500)
     for N, K, dt in ((33, 100, orc.HALF), (64, 4096, orc.BF16)):
