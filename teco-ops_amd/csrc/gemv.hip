@@ -551,6 +551,16 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
         const int row = min(idx / kx, B - 1);
         xr[j] = x[static_cast<long long>(row) * kx + idx % kx];
     }
+    // int8 W on a full-GPU grid: every CU's x loads miss L2 together and, at
+    // HBM, queue behind the first W loads of all waves, which start at the
+    // same moment, while no wave can use its W before x is in LDS.  Pausing
+    // ~1000 cycles before the W loads lets the x misses reach HBM first
+    // (batch 8 x [14336, 4096], A/B on two boxes: 13.4 -> 12.9 us and
+    // 14.0 -> 13.8 us; waiting for x outright: 14.0 us; fp16 W, twice the
+    // bytes per x byte, gains nothing).
+    if constexpr (I8) {
+        if (gridDim.x >= 128) __builtin_amdgcn_s_sleep(16);
+    }
     // This lane's x chunks in LDS: chunk 16i + blk (fp16 W) or 32i + 2blk and
     // the next (int8 W) of row 4cg + r.  The swizzle xor (4r < 16) stays below
     // the step's bits, so xs_chunk(4cg + r, c0 + 16i, K) = xs_chunk(4cg + r,
