@@ -11,8 +11,10 @@
 // into LDS and shared by all H + Hkv heads; each lane then rotates 8 NeoX
 // pairs per task with two 16-byte loads and stores (4 pairs with 8-byte words
 // when only 8-byte alignment holds; 4 GPT-J pairs per 16-byte word), streamed
-// with the non-temporal policy.  HBM-bound: every byte of q and k is read
-// once and written once.
+// with the non-temporal policy.  On the 16-byte NeoX path a thread issues the
+// loads of several tasks before any store (one memory round trip per batch
+// instead of per task).  HBM-bound: every byte of q and k is read once and
+// written once.
 #include "common.h"
 #include "device.h"
 
@@ -24,6 +26,8 @@ constexpr int kThreads = 256;
 constexpr int kMaxHalf = 256;  // rot_dim <= 512
 
 constexpr int kTokensPerBlock = 4;
+constexpr int kRotBatch = 6;  // rotation tasks per thread with loads in flight together
+constexpr int kFusedBatch = 8;  // tasks per thread in flight together, fused kernel
 
 // o1 = x1 cos - x2 sin, o2 = x2 cos + x1 sin with the roundings spelled out
 // (one product, then one fused multiply-add), so every kernel that rotates
@@ -130,6 +134,44 @@ rotary_kernel(const int64_t *__restrict__ positions, uint16_t *__restrict__ quer
     const int tasks_per_head = half / P;
     const int heads = num_heads + (key ? num_kv_heads : 0);
     const int per_token = heads * tasks_per_head;
+    if constexpr (NEOX && VW == 2) {
+        // A thread's tasks (threadIdx.x + kThreads * u) load their 16-byte
+        // words kRotBatch at a time before any rotation or store, so each
+        // pass costs one memory round trip instead of one per task.  The
+        // loads are unconditional, at the last task / token when past the
+        // end, so the compiler waits for each at its use.
+        const int total = kTokensPerBlock * per_token;
+        for (int base = threadIdx.x; base < total; base += kThreads * kRotBatch) {
+            uint4 xa[kRotBatch], xb[kRotBatch];
+            uint16_t *rp[kRotBatch];
+            int ci[kRotBatch];  // cs offset of the task's first pair, or -1: no store
+#pragma unroll
+            for (int u = 0; u < kRotBatch; ++u) {
+                const int task = min(base + kThreads * u, total - 1);
+                const int tt = task / per_token;
+                const int local0 = task - tt * per_token;
+                const bool is_q = local0 < num_heads * tasks_per_head;
+                const int local = is_q ? local0 : local0 - num_heads * tasks_per_head;
+                const int h = local / tasks_per_head;
+                const int i0 = (local - h * tasks_per_head) * P;
+                const long long t = min(tbase + tt, num_tokens - 1);
+                uint16_t *row = (is_q ? query + t * q_stride : key + t * k_stride) + h * head_size + i0;
+                rp[u] = row;
+                xa[u] = ld_stream(reinterpret_cast<const uint4 *>(row));
+                xb[u] = ld_stream(reinterpret_cast<const uint4 *>(row + half));
+                ci[u] = (base + kThreads * u < total && !skip[tt]) ? tt * kMaxHalf + i0 : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < kRotBatch; ++u) {
+                if (ci[u] < 0) continue;
+                uint4 oa, ob;
+                rot_neox8<T>(xa[u], xb[u], &cs[0][0] + ci[u], oa, ob);
+                st_stream(reinterpret_cast<uint4 *>(rp[u]), oa);
+                st_stream(reinterpret_cast<uint4 *>(rp[u] + half), ob);
+            }
+        }
+        return;
+    }
     for (int task = threadIdx.x; task < kTokensPerBlock * per_token; task += blockDim.x) {
         const int tt = task / per_token;
         if (skip[tt]) continue;
@@ -246,6 +288,82 @@ __global__ void __launch_bounds__(kThreads) rotary_cache_kernel(FusedArgs a) {
     const int nk = a.num_kv_heads * (rot_tasks + tail_tasks);
     const int per_token = nq + nk + a.num_kv_heads * v_tasks;
     const long long head_stride = static_cast<long long>(a.block_size) * D;  // cache, per kv head
+    if constexpr (NEOX && VW == 2) {
+        if (tail_tasks == 0) {
+            // As in rotary_kernel: each pass loads the 16-byte words of
+            // kFusedBatch tasks of this thread before any rotation or store.
+            // Every task issues two unconditional loads from selected
+            // addresses (a value copy loads its word twice), clamped to the
+            // last task / token past the end.
+            const int total = kTokensPerBlock * per_token;
+            for (int base = threadIdx.x; base < total; base += kThreads * kFusedBatch) {
+                uint4 xa[kFusedBatch], xb[kFusedBatch];
+                uint16_t *d0[kFusedBatch];  // in-place row (q, or k when write_key) or null
+                uint16_t *d1[kFusedBatch];  // cache row or null
+                int ci[kFusedBatch];        // cs offset of the first pair; -1: value copy
+#pragma unroll
+                for (int u = 0; u < kFusedBatch; ++u) {
+                    const int task = min(base + kThreads * u, total - 1);
+                    const int tt = task / per_token;
+                    const int t = tbase + tt;
+                    const long long tl = min(t, a.num_tokens - 1);
+                    const bool live = base + kThreads * u < total && t < a.num_tokens;
+                    const long long cr = crow[tt];
+                    int local = task - tt * per_token;
+                    const uint16_t *s0, *s1;
+                    uint16_t *w0 = nullptr, *w1 = nullptr;
+                    int c = -1;
+                    if (local < nq) {  // query head: rotate in place
+                        const int h = local / rot_tasks;
+                        const int i0 = (local - h * rot_tasks) * P;
+                        uint16_t *row = a.query + tl * a.q_stride + h * D + i0;
+                        s0 = row;
+                        s1 = row + half;
+                        w0 = row;
+                        c = tt * kMaxHalf + i0;
+                    } else if ((local -= nq) < nk) {  // key head: rotate, cache (and write back)
+                        const int h = local / rot_tasks;
+                        const int i0 = (local - h * rot_tasks) * P;
+                        uint16_t *row = a.key + tl * a.k_stride + h * D + i0;
+                        s0 = row;
+                        s1 = row + half;
+                        if (a.write_key) w0 = row;
+                        if (cr >= 0) w1 = a.kcache + cr + h * head_stride + i0;
+                        c = tt * kMaxHalf + i0;
+                    } else {  // value head: copy into the cache
+                        local -= nk;
+                        const int h = local / v_tasks;
+                        const int e0 = (local - h * v_tasks) * CV;
+                        s0 = s1 = a.value + tl * a.v_stride + h * D + e0;
+                        if (cr >= 0) w1 = a.vcache + cr + h * head_stride + e0;
+                    }
+                    xa[u] = ld_stream(reinterpret_cast<const uint4 *>(s0));
+                    xb[u] = ld_stream(reinterpret_cast<const uint4 *>(s1));
+                    d0[u] = live ? w0 : nullptr;
+                    d1[u] = live ? w1 : nullptr;
+                    ci[u] = c;
+                }
+#pragma unroll
+                for (int u = 0; u < kFusedBatch; ++u) {
+                    if (ci[u] < 0) {
+                        if (d1[u] != nullptr) st_stream(reinterpret_cast<uint4 *>(d1[u]), xa[u]);
+                        continue;
+                    }
+                    uint4 oa, ob;
+                    rot_neox8<T>(xa[u], xb[u], &cs[0][0] + ci[u], oa, ob);
+                    if (d0[u] != nullptr) {
+                        st_stream(reinterpret_cast<uint4 *>(d0[u]), oa);
+                        st_stream(reinterpret_cast<uint4 *>(d0[u] + half), ob);
+                    }
+                    if (d1[u] != nullptr) {
+                        st_stream(reinterpret_cast<uint4 *>(d1[u]), oa);
+                        st_stream(reinterpret_cast<uint4 *>(d1[u] + half), ob);
+                    }
+                }
+            }
+            return;
+        }
+    }
     for (int task = threadIdx.x; task < kTokensPerBlock * per_token; task += blockDim.x) {
         const int tt = task / per_token;
         const int t = tbase + tt;

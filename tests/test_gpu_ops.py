@@ -185,7 +185,8 @@ def test_rotary_partial_rot_dim_bf16_and_scalar_path():
 
 
 def _run_rotary_cache(T, H, Hkv, D, NB, BS, seed, is_neox=True, use_cache=False,
-                      dtype=orc.HALF, rot_dim=None, write_key=False, maxpos=2048):
+                      dtype=orc.HALF, rot_dim=None, write_key=False, maxpos=2048,
+                      oob_positions=False):
     """Fused decode step against (a) rotary_embedding then reshape_and_cache on
     the GPU (bit-exact: same arithmetic) and (b) the oracle (q and cached k
     within tolerance, cached v bit-exact)."""
@@ -195,6 +196,8 @@ def _run_rotary_cache(T, H, Hkv, D, NB, BS, seed, is_neox=True, use_cache=False,
     v = bits(r.standard_normal((T, Hkv, D)), dtype)
     pos = (np.arange(T) % maxpos).astype(np.int64)
     r.shuffle(pos)
+    if oob_positions:
+        pos[::5] = maxpos + 3        # past the cos/sin cache: cached unrotated
     slots = r.permutation(NB * BS)[:T].astype(np.int64)
     slots[::7] = -1                  # skipped
     slots[3::11] = NB * BS + 5       # past the cache: skipped
@@ -252,6 +255,16 @@ def test_rotary_reshape_and_cache_variants(is_neox, use_cache):
 def test_rotary_reshape_and_cache_partial_bf16_scalar_write_key():
     _run_rotary_cache(64, 3, 1, 64, 12, 8, seed=22, rot_dim=32, dtype=orc.BF16, write_key=True)
     _run_rotary_cache(50, 3, 2, 20, 10, 5, seed=23, rot_dim=10, write_key=True)  # scalar path
+
+
+@pytest.mark.parametrize("write_key", [True, False])
+def test_rotary_reshape_and_cache_batched_edges(write_key):
+    """NeoX 16-byte fused path with rot_dim = head_size (each thread loads a
+    batch of tasks before storing): 301 tokens leave a partial last
+    workgroup, every fifth position lies past the cos/sin cache, and skipped
+    slots mix with cached ones in every batch."""
+    _run_rotary_cache(301, 8, 2, 128, 60, 16, seed=26 + write_key, use_cache=True,
+                      write_key=write_key, oob_positions=True)
 
 
 def test_rotary_reshape_and_cache_baseline_shape():
