@@ -10,7 +10,7 @@
 // gfx950 design: 16-byte chunks of (token, head) rows; each load instruction
 // of a wave covers 1 KiB of contiguous key (and value) bytes, so reads are
 // fully coalesced and every destination run is a whole head_size row.  Each
-// lane moves 8 key and 8 value chunks with every load in flight before the
+// lane moves 4 key and 4 value chunks with every load in flight before the
 // first store (non-temporal, read and written once).
 // HBM-bound: algorithmic bytes = 4 * num_tokens * H * D * 2 + 8 * num_tokens.
 #include "common.h"
@@ -81,9 +81,10 @@ tecoopsStatus_t launch(tecoopsHandle_t handle, const void *key, const void *valu
         return TECOOPS_STATUS_NOT_SUPPORTED;
     }
     const int lbs = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
-    // 8 chunks per lane, all loaded before the scattered stores: 12.6 us at
-    // 8192 tokens x 8 heads x 128 (14.9 us with one chunk per lane)
-    constexpr int U = 8;
+    // 4 chunks per lane, all loaded before the scattered stores: 12.2 us at
+    // 8192 tokens x 8 heads x 128 (2 / 8 / 16 chunks: 13.6 / 12.3 / 13.5 us;
+    // plain instead of non-temporal stores: 12.8 us)
+    constexpr int U = 4;
     auto *kern = lbs >= 0 ? &reshape_and_cache_kernel<V, true, U> : &reshape_and_cache_kernel<V, false, U>;
     // lane indices are 32-bit: tokens run in slices of fewer than 2^30 lanes
     const int slice = static_cast<int>((1ll << 30) / per_token);
