@@ -719,8 +719,8 @@ constexpr int kRI8 = 2, kCplI8 = 4;
 // workgroup, so workgroups are large (b8_waves picks their size).  Measured
 // at batch 8 on [14336, 4096], same box: int8 with 1, 2, 3, 4, 8 and 16
 // steps in flight took 16.5, 12.6, 13.1, 14.9, 15.9 and 16.3 us (2 row
-// groups per wave: 15.0-15.6 us); fp16 with 2, 4 and 8 took 22.0, 22.5 and
-// 20.9 us.
+// groups per wave: 15.0-15.6 us); fp16 with 2, 4, 6, 8, 10, 12 and 16 took
+// 22.0, 22.5, 21.7, 20.8, 20.9, 21.2 and 20.8 us.
 constexpr int kB8RgF16 = 1, kB8CplF16 = 8, kB8RgI8 = 1, kB8CplI8 = 2;
 constexpr int kB8MaxBatch = 8;
 
