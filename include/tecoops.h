@@ -152,10 +152,15 @@ tecoopsStatus_t tecoopsRmsNorm(tecoopsHandle_t handle,
  *      [batch, max_blocks_per_seq]; q_seq_lens / kv_seq_lens int32 [batch]
  *      (device).  Scale is 1/sqrt(D).  Element type comes from the
  *      descriptors: TECOOPS_DATA_HALF or TECOOPS_DATA_BFLOAT16 (q, caches and
- *      output must agree).  D in {64, 128}; any block_size >= 1.
- *      max_seqlen_q and max_seqlen_k must bound every q / kv length.
- *      workspace may be NULL (the handle then owns the split-KV scratch) or
- *      point to tecoopsGetFlashAttentionWorkspaceSize() bytes. ---- */
+ *      output must agree).  D in {32, 64, 96, 128, 160, 192}; any
+ *      block_size >= 1.  As in the reference, the results do not depend on
+ *      max_seqlen_q / max_seqlen_k (any value, also <= 0, is accepted): they
+ *      only shape the launch, and a bound that holds makes it fastest.
+ *      kv lengths past block_table_dim * block_size (the reference's
+ *      precondition) are clamped to it.  max_block_num and workspace are
+ *      accepted and ignored, as in the reference (flash_attention.cpp:110):
+ *      the split-KV partials of decode live in the handle's scratch, one
+ *      buffer per stream the handle runs on. ---- */
 tecoopsStatus_t tecoopsFlashAttention(tecoopsHandle_t handle,
                                       int max_seqlen_q, int max_seqlen_k,
                                       int max_block_num, const int *q_seq_lens,
@@ -210,7 +215,11 @@ tecoopsStatus_t tecoopsReshapeAndCacheEx(tecoopsHandle_t handle,
 /* Flash attention with the arguments the reference's torch wrapper accepts but
  * drops (api/torch_ext.cpp:99-165): cu_seqlens_q int32 [batch+1] (device) is
  * used when q_seq_lens is NULL, so callers need no host synchronisation;
- * softmax_scale > 0 overrides 1/sqrt(D); causal = 0 disables the mask. */
+ * softmax_scale > 0 overrides 1/sqrt(D); causal = 0 disables the mask.
+ * workspace NULL uses the handle's scratch; otherwise it must hold
+ * tecoopsGetFlashAttentionWorkspaceSize() bytes for the same batch, heads,
+ * head size, max_seqlen_q and max_seqlen_k, and max_seqlen_k must then be > 0
+ * (it sizes the split-KV partials). */
 tecoopsStatus_t tecoopsFlashAttentionEx(tecoopsHandle_t handle,
                                         int max_seqlen_q, int max_seqlen_k,
                                         const int *q_seq_lens, const int *cu_seqlens_q,
@@ -227,7 +236,9 @@ tecoopsStatus_t tecoopsFlashAttentionEx(tecoopsHandle_t handle,
                                         void *oData, float softmax_scale, int causal,
                                         void *workspace);
 
-/* Bytes of split-KV scratch tecoopsFlashAttention may use for these sizes. */
+/* Bytes of caller workspace tecoopsFlashAttentionEx needs for these sizes
+ * (max_seqlen_k > 0; max_seqlen_q <= 0 sizes for the longest q length the
+ * split-KV decode route takes). */
 tecoopsStatus_t tecoopsGetFlashAttentionWorkspaceSize(int batch, int num_heads,
                                                       int head_size, int max_seqlen_q,
                                                       int max_seqlen_k, size_t *bytes);

@@ -19,6 +19,16 @@ OUT = os.path.join(HERE, "tecoops", "libtecoops.so")
 TORCH_OUT = os.path.join(HERE, "tecoops", "libtecoops_torch.so")
 PLUGIN_OUT = os.path.join(HERE, "tecoops", "libtecoops_plugin.so")
 PLUGIN_SOURCES = ["plugin/registry.cpp", "plugin/plugins.cpp"]
+# The reference's artefact names (teco/CMakeLists.txt:99-129): libteco_ops.so
+# (the operator library of the torch build), libteco_ops_plugin.so (the same
+# library in the plugin build) and libTecoInferPlugin.so (the plugins, linked
+# against it).  Each is a link to the library built here that holds the same
+# interface, so a caller linked against a reference name loads this build.
+REFERENCE_NAMES = {
+    "libteco_ops.so": "libtecoops.so",
+    "libteco_ops_plugin.so": "libtecoops.so",
+    "libTecoInferPlugin.so": "libtecoops_plugin.so",
+}
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 SOURCES = [
@@ -104,6 +114,16 @@ def build_plugins(verbose=False):
     return PLUGIN_OUT
 
 
+def link_reference_names():
+    """(Re)creates the reference-named links next to the built libraries."""
+    d = os.path.dirname(OUT)
+    for name, target in REFERENCE_NAMES.items():
+        path = os.path.join(d, name)
+        if os.path.lexists(path):
+            os.remove(path)
+        os.symlink(target, path)
+
+
 def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     jobs = min(len(SOURCES), os.cpu_count() or 4, 16)
@@ -121,6 +141,7 @@ def build(verbose=False):
     os.replace(tmp, OUT)
     build_plugins(verbose)
     build_torch_ext(verbose)
+    link_reference_names()
     return OUT
 
 

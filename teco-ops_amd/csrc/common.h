@@ -3,9 +3,13 @@
 // The handle replaces the reference's tecoopsContext{spa_num, spe_num,
 // spm_size, stream} (teco/interface/include/builtin_type.h:33-38): on gfx950
 // there is no SPA/SPE/SPM to describe, so the handle holds the HIP stream and
-// a grow-only device scratch buffer (allocated on the device current at the
-// first op that needs it) used by split-KV flash attention when the caller
-// passes no workspace.
+// the device scratch used by split-KV flash attention when the caller passes
+// no workspace.  The scratch is kept per stream (up to kScratchSlots streams,
+// least recently used replaced first): work on one stream is ordered by the
+// stream, and calls on different streams never share a buffer, so no event or
+// wait is needed.  Each buffer grows on demand on the device current at the
+// op; hipFree synchronises the device first, so a buffer still read by
+// enqueued work is never freed under it.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -17,10 +21,19 @@
 
 #include "tecoops.h"
 
+constexpr int kScratchSlots = 8;
+
+struct ScratchSlot {
+    hipStream_t stream = nullptr;
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    unsigned long long last_use = 0;
+};
+
 struct tecoopsContext {
     hipStream_t stream = nullptr;
-    void *scratch = nullptr;
-    size_t scratch_bytes = 0;
+    ScratchSlot scratch[kScratchSlots];
+    unsigned long long uses = 0;
 };
 
 // Descriptor: same fields and stride rules as the reference
@@ -94,9 +107,8 @@ inline int device_cus() {
     return v;
 }
 
-// Returns a device buffer of at least `bytes` owned by the handle.  Growing
-// synchronises the handle's stream first so a buffer still read by enqueued
-// work is never freed.
+// Returns a device buffer of at least `bytes` owned by the handle for the
+// handle's current stream, for an op about to be enqueued there.
 tecoopsStatus_t handle_scratch(tecoopsHandle_t handle, size_t bytes, void **out);
 
 }  // namespace tecoops

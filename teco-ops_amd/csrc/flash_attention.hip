@@ -40,11 +40,11 @@
 //     across workgroups (split-KV), partial (m, l, O) merged first in LDS and
 //     then by a combine kernel.  HBM-bound: every cached K/V byte is read
 //     once.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <mutex>
-#include <vector>
 
 #include "common.h"
 #include "device.h"
@@ -95,6 +95,7 @@ struct FaParams {
     const int *cu_q;     // cumulative q offsets [batch+1], used when q_lens is NULL
     const int *kv_lens;
     int batch, H, Hkv, G, bs, lbs, num_blocks;  // lbs = log2(bs) when bs is a power of 2
+    int kv_cap;          // block-table width * block_size: kv lengths are clamped to it
     long long page_stride;                      // Hkv * bs * D elements per cache block
     float scale_log2;    // softmax_scale * log2(e)
     int causal;
@@ -120,6 +121,15 @@ __device__ __forceinline__ void seq_info(const FaParams &p, int b, long long &q_
         q_off = off;
         L = p.q_lens[b];
     }
+}
+
+// kv length of sequence b.  The reference reads block_table[b][j / block_size]
+// for every key j < kv_len from a row of block_table_dim entries
+// (flash_attention.scpp:190, :206), so kv_len <= block_table_dim * block_size
+// is its precondition; clamping to that keeps every block-table read inside
+// the row.  A negative length counts as 0.
+__device__ __forceinline__ int kv_len(const FaParams &p, int b) {
+    return min(max(p.kv_lens[b], 0), p.kv_cap);
 }
 
 // 16-byte K/V load; STREAM selects the non-temporal policy for data read once.
@@ -157,9 +167,11 @@ __device__ __forceinline__ long long row_offset(const FaParams &p, const int *bt
 }
 
 // Cooperative global -> register -> LDS staging of one TILE-key K/V tile by NT
-// threads.  K is stored row-major [TILE][D + 8]; V transposed [D][TILE + 4].
-// Each thread owns one 16-byte column of K (rows r0, r0 + KRS, ...) and
-// VPT (4-row x 8-column) blocks of V.
+// threads, for any head size D that is a multiple of 32.  K is stored
+// row-major [TILE][D + 8]; V transposed [D][TILE + 4].  The TILE * D/8
+// 16-byte chunks of K are dealt to the threads in order (chunk tid + i*NT is
+// row / column (tid + i*NT) / (D/8), % (D/8)); each thread also owns VPT
+// (4-row x 8-column) blocks of V.
 template <int D, int TILE, int NT, bool POW2, bool STREAM = false>
 struct TileLoader {
     static constexpr int KP = D + 8;
@@ -167,10 +179,9 @@ struct TileLoader {
     static constexpr int ELEMS = TILE * KP + D * VP;  // one K + V^T buffer
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int KCH = TILE * CPR / NT;
-    static constexpr int KRS = NT / CPR;
     static constexpr int VTASKS = (TILE / 4) * CPR;
     static constexpr int VPT = (VTASKS + NT - 1) / NT;
-    static_assert(TILE * CPR % NT == 0 && NT % CPR == 0, "K tile must split evenly");
+    static_assert(D % 32 == 0 && TILE * CPR % NT == 0, "K tile must split evenly");
     u32x4 k[KCH];
     u32x4 v[VPT][4];
     uint32_t vok;  // bit 4i+r: V row of v[i][r] is valid (below kv_limit, page in range)
@@ -180,13 +191,13 @@ struct TileLoader {
     __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
                                          int j0, int kv_limit) {
         const int tid = threadIdx.x;
-        const int col = tid % CPR, r0 = tid / CPR;
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
+            const int task = tid + i * NT;
             bool ok;
-            const long long o = row_offset<D, POW2>(p, bt_row, head_off, j0 + r0 + i * KRS,
+            const long long o = row_offset<D, POW2>(p, bt_row, head_off, j0 + task / CPR,
                                                     kv_limit, ok);
-            k[i] = load16<STREAM>(p.kc + o + col * 8);
+            k[i] = load16<STREAM>(p.kc + o + (task % CPR) * 8);
         }
         // Invalid V rows are zeroed in store(), so the wave does not wait for
         // the loads here.
@@ -211,10 +222,11 @@ struct TileLoader {
         uint16_t *Ks = buf;
         uint16_t *Vt = buf + TILE * KP;
         const int tid = threadIdx.x;
-        const int col = tid % CPR, r0 = tid / CPR;
 #pragma unroll
-        for (int i = 0; i < KCH; ++i)
-            *reinterpret_cast<u32x4 *>(Ks + (r0 + i * KRS) * KP + col * 8) = k[i];
+        for (int i = 0; i < KCH; ++i) {
+            const int task = tid + i * NT;
+            *reinterpret_cast<u32x4 *>(Ks + (task / CPR) * KP + (task % CPR) * 8) = k[i];
+        }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int task = tid + i * NT;
@@ -490,36 +502,18 @@ constexpr size_t prefill_lds_bytes() {
     return 2 * sizeof(uint16_t) * (TILE * (D + 8) + D * (TILE + 4));
 }
 
-// Workgroup (b, kv head, head group, query tile) with W waves: wave w serves
-// query head hg*HW + w % HW of the GQA group and query rows
-// [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of TILE keys are double
-// buffered in LDS (one barrier per tile) and attended 32 * NKB keys at a time.
-// W >= 12 asks for 3 waves per SIMD (168 VGPRs), else 2.
+// One query tile [q0, q0 + QT) of workgroup (b, kv head kvh, head group hg):
+// the body of fa_prefill_kernel.  Ends with a barrier, so the LDS tile
+// buffers can be refilled by the next call.
 template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
-__global__ void __launch_bounds__(W * 64, W >= 12 ? 3 : 2)
-fa_prefill_kernel(FaParams p) {
-    // keys are attended 32 * NKB at a time within a tile
+__device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, int b, int kvh,
+                                             int hg, long long q_off, int L, int S, int q0) {
     constexpr int NKB = TILE % 64 == 0 ? 2 : 1;
     constexpr int KB = 32 * NKB;
     using Loader = typename LoaderSel<D, TILE, W, POW2>::type;
     constexpr int KP = Loader::KP, VP = Loader::VP;
     constexpr int WROWS = 32 * QSUB;
     constexpr int QT = WROWS * (W / HW);
-    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-
-    int bx = blockIdx.x;
-    const int ngroups = p.G / HW;
-    const int hg = bx % ngroups;
-    bx /= ngroups;
-    const int kvh = bx % p.Hkv;
-    const int b = bx / p.Hkv;
-    const int tile = gridDim.y - 1 - blockIdx.y;  // heaviest causal tiles first
-    long long q_off;
-    int L;
-    seq_info(p, b, q_off, L);
-    const int q0 = tile * QT;
-    if (q0 >= L) return;
-    const int S = p.kv_lens[b];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 5, r32 = lane & 31;
     const int h = kvh * p.G + hg * HW + (wave % HW);
@@ -606,6 +600,58 @@ fa_prefill_kernel(FaParams p) {
     }
 }
 
+// Workgroup (b, kv head, head group, query tile) with W waves: wave w serves
+// query head hg*HW + w % HW of the GQA group and query rows
+// [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of TILE keys are double
+// buffered in LDS (one barrier per tile) and attended 32 * NKB keys at a time.
+// W >= 12 asks for 3 waves per SIMD (168 VGPRs); head sizes above 128 one
+// workgroup per CU (their LDS tiles allow no more); else 2.
+template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
+__global__ void __launch_bounds__(W * 64, W >= 12 ? 3 : (D > 128 ? 1 : 2))
+fa_prefill_kernel(FaParams p) {
+    constexpr int QT = 32 * QSUB * (W / HW);
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    int bx = blockIdx.x;
+    const int ngroups = p.G / HW;
+    const int hg = bx % ngroups;
+    bx /= ngroups;
+    const int kvh = bx % p.Hkv;
+    const int b = bx / p.Hkv;
+    long long q_off;
+    int L;
+    seq_info(p, b, q_off, L);
+    const int tile = gridDim.y - 1 - blockIdx.y;  // heaviest causal tiles first
+    if (tile * QT >= L) return;
+    prefill_tile<T, D, W, HW, QSUB, POW2, TILE>(p, lds, b, kvh, hg, q_off, L, kv_len(p, b),
+                                                tile * QT);
+}
+
+// The query tiles from first_tile on, which fa_prefill_kernel's grid (sized
+// from max_seqlen_q, a bound the reference never reads) does not cover: one
+// workgroup per (b, kv head, head group) takes them in turn.  Launched after
+// fa_prefill_kernel whenever a q_len could exceed the grid; with a bound that
+// holds, every workgroup finds no tile and exits.  A kernel of its own, so
+// that fa_prefill_kernel has no loop around its tile (values hoisted out of
+// a loop would stay live across the tile and cost registers).
+template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
+__global__ void __launch_bounds__(W * 64, W >= 12 ? 3 : (D > 128 ? 1 : 2))
+fa_prefill_rest_kernel(FaParams p, int first_tile) {
+    constexpr int QT = 32 * QSUB * (W / HW);
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    int bx = blockIdx.x;
+    const int ngroups = p.G / HW;
+    const int hg = bx % ngroups;
+    bx /= ngroups;
+    const int kvh = bx % p.Hkv;
+    const int b = bx / p.Hkv;
+    long long q_off;
+    int L;
+    seq_info(p, b, q_off, L);
+    const int S = kv_len(p, b);
+    for (int t = first_tile; t * QT < L; ++t)
+        prefill_tile<T, D, W, HW, QSUB, POW2, TILE>(p, lds, b, kvh, hg, q_off, L, S, t * QT);
+}
+
 // ----------------------------------------------------------------- decode
 
 constexpr int kDecTile = 128;
@@ -615,29 +661,21 @@ constexpr size_t decode_lds_bytes() {
     return sizeof(uint16_t) * (kDecTile * (D + 8) + D * (kDecTile + 4));
 }
 
-// Workgroup (b, kv head, split): keys [split*split_len, +split_len).  Column c
-// of the MFMA tile is (head c / rq, row c % rq) of the GQA group; the 4 waves
-// take the four 32-key blocks of each 128-key tile.
+// The 4 waves of a decode workgroup attend keys [kv_lo, kv_hi) of (sequence
+// b, kv head kvh) for the query rows [r0, r0 + rq): column c of the MFMA tile
+// is (head c / rq, row r0 + c % rq) of the GQA group and wave w takes keys
+// [32w, 32w + 32) of each 128-key tile.  Leaves each wave's partial state in
+// LDS, after a barrier: max lm[4][32], sum ll[4][32] and unnormalised O
+// lo[4][32][D] (fp32, over the tile buffers).
 template <typename T, int D, bool POW2>
-__global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
+__device__ __forceinline__ void decode_pass(const FaParams &p, uint16_t *smem, int b, int kvh,
+                                            long long q_off, int L, int S, int kv_lo, int kv_hi,
+                                            int rq, int r0) {
     using Loader = typename LoaderSel<D, kDecTile, 4, POW2, true>::type;
     constexpr int KP = Loader::KP, VP = Loader::VP;
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-
-    const int kvh = blockIdx.x % p.Hkv;
-    const int b = blockIdx.x / p.Hkv;
-    const int split = blockIdx.y;
-    long long q_off;
-    int L;
-    seq_info(p, b, q_off, L);
-    if (L <= 0) return;
-    const int S = p.kv_lens[b];
-    const int kv_lo = split * p.split_len;
-    if (split > 0 && kv_lo >= S) return;
-    const int kv_hi = min(S, kv_lo + p.split_len);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 5, r32 = lane & 31;
-    const int hl = r32 / p.rq, row = r32 % p.rq;
+    const int hl = r32 / rq, row = r0 + r32 % rq;
     const bool col_ok = hl < p.G && row < L;
     const int h = kvh * p.G + min(hl, p.G - 1);
     const int q_start = p.causal ? max(S - L, 0) : 0;
@@ -654,8 +692,9 @@ __global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
             qf[0][ks] = col_ok ? x : zero;
         }
     }
+    // keys visible to this column, and to the pass's first row (the fewest)
     const int vis = min(kv_hi, p.causal ? q_start + row + 1 : S);
-    const int min_vis = min(kv_hi, p.causal ? q_start + 1 : S);
+    const int min_vis = min(kv_hi, p.causal ? q_start + r0 + 1 : S);
 
     float m[1] = {0.0f}, lsum[1] = {0.0f};
     f32x16_t oacc[1][D / 32];
@@ -688,7 +727,6 @@ __global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
         }
     }
 
-    // Merge the 4 waves' partial states in LDS (reusing the tile buffers).
     __syncthreads();
     float *lm = reinterpret_cast<float *>(smem);   // [4][32] max
     float *ll = lm + 4 * 32;                        // [4][32] sum
@@ -706,8 +744,17 @@ __global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
             lo[(wave * 32 + r32) * D + d] = oacc[0][db][v];
         }
     __syncthreads();
-    const long long base = (static_cast<long long>(b) * p.Hkv + kvh) * p.max_splits + split;
-    for (int task = threadIdx.x; task < p.ncols * D; task += blockDim.x) {
+}
+
+// Merges the 4 waves' partial states that decode_pass left in LDS, one thread
+// per (column, d) of the first ncols columns: sink(c, d, O, m, l) receives the
+// column's merged unnormalised O[d], max and sum.
+template <int D, typename Sink>
+__device__ __forceinline__ void merge_waves(const uint16_t *smem, int ncols, Sink sink) {
+    const float *lm = reinterpret_cast<const float *>(smem);
+    const float *ll = lm + 4 * 32;
+    const float *lo = ll + 4 * 32;
+    for (int task = threadIdx.x; task < ncols * D; task += blockDim.x) {
         const int c = task / D, d = task % D;
         float M = lm[c];
 #pragma unroll
@@ -719,12 +766,60 @@ __global__ void __launch_bounds__(256, 2) fa_decode_kernel(FaParams p) {
             acc += f * lo[(w * 32 + c) * D + d];
             lsum_all += f * ll[w * 32 + c];
         }
-        p.ws_o[(base * p.ncols + c) * D + d] = acc;
-        if (d == 0) {
-            p.ws_ml[(base * p.ncols + c) * 2] = M;
-            p.ws_ml[(base * p.ncols + c) * 2 + 1] = lsum_all;
-        }
+        sink(c, d, acc, M, lsum_all);
     }
+}
+
+// Workgroup (b, kv head, split): keys [split*split_len, +split_len), the last
+// split also every key past the splits (the host sizes the splits from
+// max_seqlen_k, which the reference never reads).  Its rows' partial (m, l, O)
+// go to the workspace for fa_decode_combine_kernel.
+//
+// The host routes to this kernel when G * max_seqlen_q <= 32 and lays the
+// columns out for rq = max_seqlen_q rows.  A sequence with more rows than
+// that is attended here in full by its split-0 workgroup instead, 32 / G rows
+// per pass over all its keys, which writes its output rows itself; the
+// combine kernel leaves it alone.  So the output never depends on the host's
+// bounds, only the speed does.
+template <typename T, int D, bool POW2>
+__global__ void __launch_bounds__(256, D > 128 ? 1 : 2) fa_decode_kernel(FaParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    const int kvh = blockIdx.x % p.Hkv;
+    const int b = blockIdx.x / p.Hkv;
+    const int split = blockIdx.y;
+    long long q_off;
+    int L;
+    seq_info(p, b, q_off, L);
+    if (L <= 0) return;
+    const int S = kv_len(p, b);
+    if (L > p.rq) {
+        if (split != 0) return;
+        const int rq = 32 / p.G;
+        for (int r0 = 0; r0 < L; r0 += rq) {
+            decode_pass<T, D, POW2>(p, smem, b, kvh, q_off, L, S, 0, S, rq, r0);
+            merge_waves<D>(smem, p.G * rq, [&](int c, int d, float acc, float, float l) {
+                const int hl = c / rq, row = r0 + c % rq;
+                if (row >= L) return;
+                const int h = kvh * p.G + hl;
+                p.o[((q_off + row) * p.H + h) * D + d] = Cvt<T>::from(l > 0.0f ? acc / l : 0.0f);
+            });
+            __syncthreads();  // the next pass refills the LDS
+        }
+        return;
+    }
+    const int kv_lo = split * p.split_len;
+    if (split > 0 && kv_lo >= S) return;
+    const int kv_hi = split == static_cast<int>(gridDim.y) - 1 ? S : min(S, kv_lo + p.split_len);
+    decode_pass<T, D, POW2>(p, smem, b, kvh, q_off, L, S, kv_lo, kv_hi, p.rq, 0);
+    const long long base = ((static_cast<long long>(b) * p.Hkv + kvh) * p.max_splits + split) *
+                           p.ncols;
+    merge_waves<D>(smem, p.ncols, [&](int c, int d, float acc, float M, float l) {
+        p.ws_o[(base + c) * D + d] = acc;
+        if (d == 0) {
+            p.ws_ml[(base + c) * 2] = M;
+            p.ws_ml[(base + c) * 2 + 1] = l;
+        }
+    });
 }
 
 // Merges the split partials of (b, kv head) into the output rows.  The
@@ -743,8 +838,8 @@ __global__ void __launch_bounds__(256) fa_decode_combine_kernel(FaParams p) {
     long long q_off;
     int L;
     seq_info(p, b, q_off, L);
-    if (L <= 0) return;
-    const int S = p.kv_lens[b];
+    if (L <= 0 || L > p.rq) return;  // L > rq: written by fa_decode_kernel
+    const int S = kv_len(p, b);
     int nsplit = S <= 0 ? 1 : (S + p.split_len - 1) / p.split_len;
     nsplit = min(nsplit, p.max_splits);
     const long long base = (static_cast<long long>(b) * p.Hkv + kvh) * p.max_splits;
@@ -810,26 +905,31 @@ __global__ void __launch_bounds__(256) fa_decode_combine_kernel(FaParams p) {
 
 // ------------------------------------------------------------------- host
 
+// Launch shape.  rq is the host's bound on q_len (routing and grid height),
+// split_len / max_splits the split-KV plan from its bound on kv_len.  Neither
+// bound changes the output (the kernels also cover longer sequences), only
+// the speed.
 struct Plan {
     bool decode;
     int rq, ncols, split_len, max_splits;
+    long long total_q;  // sum of the q lengths (q's descriptor): bounds every q_len
 };
 
-Plan make_plan(int batch, int H, int Hkv, int max_q, int max_k) {
+Plan make_plan(int batch, int H, int Hkv, int q_hint, int k_hint) {
     Plan pl{};
     const int G = H / Hkv;
-    pl.decode = max_q >= 1 && G * max_q <= 32;
-    pl.rq = max_q;
-    pl.ncols = G * max_q;
+    pl.decode = q_hint >= 1 && G * q_hint <= 32;
+    pl.rq = q_hint;
+    pl.ncols = G * q_hint;
     // Split the key range so that the grid has at least ~2048 workgroups, with
     // splits as long as that allows (up to 2048 keys): at B=64, Hkv=8 and
     // kv_len <= 8192, 2048-key splits ran in 194 us against 217 us at 512
     // (fewer partials to write and merge; the merge kernel is a fixed cost).
     const long long units = static_cast<long long>(batch) * Hkv;
     int split = 2048;
-    while (split > kDecTile && units * ((max_k + split - 1) / split) < 2048) split >>= 1;
+    while (split > kDecTile && units * ((k_hint + split - 1) / split) < 2048) split >>= 1;
     pl.split_len = split;
-    pl.max_splits = max_k <= 0 ? 1 : (max_k + split - 1) / split;
+    pl.max_splits = k_hint <= 0 ? 1 : (k_hint + split - 1) / split;
     return pl;
 }
 
@@ -840,46 +940,60 @@ size_t workspace_bytes(const Plan &pl, int batch, int Hkv, int D) {
 }
 
 // Raises a kernel's dynamic-LDS limit once per process (per kernel address).
+// The kernels already raised are kept in a fixed table (no heap allocation,
+// so the allocation-free entry point can use it too); past its capacity the
+// attribute is simply set again on every launch.
 bool reserve_lds(const void *kernel, size_t bytes) {
     static std::mutex mu;
-    static std::vector<const void *> done;
+    static const void *done[256];
+    static int ndone = 0;
     if (bytes <= 64 * 1024) return true;
     std::lock_guard<std::mutex> lock(mu);
-    for (const void *k : done)
-        if (k == kernel) return true;
+    for (int i = 0; i < ndone; ++i)
+        if (done[i] == kernel) return true;
     if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(bytes)) != hipSuccess) {
         (void)hipGetLastError();
         TECO_ERROR("flash_attention: cannot reserve %zu bytes of LDS", bytes);
         return false;
     }
-    done.push_back(kernel);
+    if (ndone < 256) done[ndone++] = kernel;
     return true;
 }
 
+// Prefill over a grid of ceil(q_hint / QT) query tiles per (b, kv head, head
+// group), then, unless q_hint already bounds every q_len (it is at least the
+// total q length), fa_prefill_rest_kernel for the tiles past the grid.
 template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
-tecoopsStatus_t launch_prefill(const FaParams &p, int max_q, hipStream_t s) {
+tecoopsStatus_t launch_prefill(const FaParams &p, const Plan &pl, hipStream_t s) {
     constexpr int QT = 32 * QSUB * (W / HW);
     auto *kern = &fa_prefill_kernel<T, D, W, HW, QSUB, POW2, TILE>;
+    auto *rest = &fa_prefill_rest_kernel<T, D, W, HW, QSUB, POW2, TILE>;
     const size_t lds = prefill_lds_bytes<D, TILE>();
-    if (!reserve_lds(reinterpret_cast<const void *>(kern), lds)) return TECOOPS_STATUS_INTERNAL_ERROR;
-    dim3 grid(p.batch * p.Hkv * (p.G / HW), (max_q + QT - 1) / QT);
-    hipLaunchKernelGGL(kern, grid, dim3(W * 64), lds, s, p);
+    if (!reserve_lds(reinterpret_cast<const void *>(kern), lds) ||
+        !reserve_lds(reinterpret_cast<const void *>(rest), lds))
+        return TECOOPS_STATUS_INTERNAL_ERROR;
+    const int units = p.batch * p.Hkv * (p.G / HW);
+    const int tiles = (pl.rq + QT - 1) / QT;
+    hipLaunchKernelGGL(kern, dim3(units, tiles), dim3(W * 64), lds, s, p);
     TECO_CHECK_LAUNCH("flash_attention prefill");
+    if (static_cast<long long>(tiles) * QT < pl.total_q) {
+        hipLaunchKernelGGL(rest, dim3(units), dim3(W * 64), lds, s, p, tiles);
+        TECO_CHECK_LAUNCH("flash_attention prefill (rest)");
+    }
     return TECOOPS_STATUS_SUCCESS;
 }
 
 template <typename T, int D, int W, int QSUB, bool POW2, int TILE = 64>
-tecoopsStatus_t prefill_hw(const FaParams &p, int max_q, hipStream_t s) {
+tecoopsStatus_t prefill_hw(const FaParams &p, const Plan &pl, hipStream_t s) {
     const int G = p.G;
-    if (G % 4 == 0) return launch_prefill<T, D, W, 4, QSUB, POW2, TILE>(p, max_q, s);
-    if (G % 2 == 0) return launch_prefill<T, D, W, 2, QSUB, POW2, TILE>(p, max_q, s);
-    return launch_prefill<T, D, W, 1, QSUB, POW2, TILE>(p, max_q, s);
+    if (G % 4 == 0) return launch_prefill<T, D, W, 4, QSUB, POW2, TILE>(p, pl, s);
+    if (G % 2 == 0) return launch_prefill<T, D, W, 2, QSUB, POW2, TILE>(p, pl, s);
+    return launch_prefill<T, D, W, 1, QSUB, POW2, TILE>(p, pl, s);
 }
 
 template <typename T, int D>
-tecoopsStatus_t run(tecoopsHandle_t handle, FaParams &p, const Plan &pl, int max_q) {
-    hipStream_t s = handle->stream;
+tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
     const bool pow2 = p.lbs >= 3;  // power of two and >= 8: uniform-page loader
     if (pl.decode) {
         const size_t lds = decode_lds_bytes<D>();
@@ -893,12 +1007,35 @@ tecoopsStatus_t run(tecoopsHandle_t handle, FaParams &p, const Plan &pl, int max
         TECO_CHECK_LAUNCH("flash_attention combine");
         return TECOOPS_STATUS_SUCCESS;
     }
-    if (!pow2 || D != 128) {
-        return pow2 ? prefill_hw<T, D, 4, 1, true>(p, max_q, s)
-                    : prefill_hw<T, D, 4, 1, false>(p, max_q, s);
+    if constexpr (D == 128) {
+        // the uniform-page loader: 12 waves (3 per SIMD), 96-key tiles
+        if (pow2) return prefill_hw<T, D, 12, 1, true, 96>(p, pl, s);
     }
-    // D = 128 with the uniform-page loader: 12 waves (3 per SIMD), 96-key tiles
-    return prefill_hw<T, D, 12, 1, true, 96>(p, max_q, s);
+    return pow2 ? prefill_hw<T, D, 4, 1, true>(p, pl, s) : prefill_hw<T, D, 4, 1, false>(p, pl, s);
+}
+
+// Head sizes the kernels are built for: the reference takes the head size as
+// its K-dimension tile (BK = size_per_head, flash_attention.scpp:188, looped
+// at :347-348) in 32-column slabs, bounded by its on-chip buffers.
+constexpr int kHeadSizes[] = {32, 64, 96, 128, 160, 192};
+
+bool head_size_supported(int D) {
+    for (int d : kHeadSizes)
+        if (d == D) return true;
+    return false;
+}
+
+template <typename T>
+tecoopsStatus_t run_d(hipStream_t s, const FaParams &p, const Plan &pl, int D) {
+    switch (D) {
+        case 32: return run<T, 32>(s, p, pl);
+        case 64: return run<T, 64>(s, p, pl);
+        case 96: return run<T, 96>(s, p, pl);
+        case 128: return run<T, 128>(s, p, pl);
+        case 160: return run<T, 160>(s, p, pl);
+        case 192: return run<T, 192>(s, p, pl);
+        default: return TECOOPS_STATUS_NOT_SUPPORTED;
+    }
 }
 
 bool is_packed_rowmajor(const tecoopsTensorStruct *d) {
@@ -910,36 +1047,29 @@ bool is_packed_rowmajor(const tecoopsTensorStruct *d) {
     return true;
 }
 
-}  // namespace
+// A validated call: kernel parameters, launch shape and element type.
+struct FaCall {
+    FaParams p;
+    Plan pl;
+    int D;
+    bool bf16;
+};
 
-extern "C" tecoopsStatus_t tecoopsGetFlashAttentionWorkspaceSize(int batch, int num_heads,
-                                                                 int head_size, int max_seqlen_q,
-                                                                 int max_seqlen_k, size_t *bytes) {
-    if (bytes == nullptr || batch <= 0 || num_heads <= 0 || head_size <= 0 || max_seqlen_q <= 0 ||
-        max_seqlen_k < 0)
-        return TECOOPS_STATUS_BAD_PARAM;
-    // Worst case over kv-head counts: ncols * Hkv = H * max_q columns per split.
-    size_t worst = 0;
-    for (int hkv = 1; hkv <= num_heads; ++hkv) {
-        if (num_heads % hkv) continue;
-        const Plan pl = make_plan(batch, num_heads, hkv, max_seqlen_q, max_seqlen_k);
-        const size_t b = workspace_bytes(pl, batch, hkv, head_size);
-        if (b > worst) worst = b;
-    }
-    *bytes = worst;
-    return TECOOPS_STATUS_SUCCESS;
-}
-
-extern "C" tecoopsStatus_t tecoopsFlashAttentionEx(
-    tecoopsHandle_t handle, int max_seqlen_q, int max_seqlen_k, const int *q_seq_lens,
-    const int *cu_seqlens_q, const int *kv_seq_lens, const tecoopsTensorDescriptor_t btDesc,
-    const void *blockTable, const tecoopsTensorDescriptor_t qDesc, const void *qData,
-    const tecoopsTensorDescriptor_t kDesc, const void *kCache,
-    const tecoopsTensorDescriptor_t vDesc, const void *vCache,
-    const tecoopsTensorDescriptor_t oDesc, void *oData, float softmax_scale, int causal,
-    void *workspace) {
-    // Checks of reference flash_attention.cpp:44-69, extended to bf16 and to
-    // the shape facts the kernels rely on.
+// Argument checks of reference flash_attention.cpp:44-69, extended to bf16 and
+// to the shape facts the kernels rely on; fills everything but the split-KV
+// workspace.  max_seqlen_q / max_seqlen_k are launch-shape hints only: values
+// <= 0 are accepted (the reference never reads them) and replaced by bounds
+// the host knows, the mean q length (sum(q) / batch from q's descriptor) and
+// the block-table width * block_size.  fixed_k_hint keeps max_seqlen_k as
+// given, for a caller workspace sized by tecoopsGetFlashAttentionWorkspaceSize.
+tecoopsStatus_t fa_prepare(tecoopsHandle_t handle, int max_seqlen_q, int max_seqlen_k,
+                           const int *q_seq_lens, const int *cu_seqlens_q, const int *kv_seq_lens,
+                           const tecoopsTensorDescriptor_t btDesc, const void *blockTable,
+                           const tecoopsTensorDescriptor_t qDesc, const void *qData,
+                           const tecoopsTensorDescriptor_t kDesc, const void *kCache,
+                           const tecoopsTensorDescriptor_t vDesc, const void *vCache,
+                           const tecoopsTensorDescriptor_t oDesc, void *oData, float softmax_scale,
+                           int causal, bool fixed_k_hint, FaCall &c) {
     if (handle == nullptr) return TECOOPS_STATUS_NOT_INITIALIZED;
     if (!btDesc || !qDesc || !kDesc || !vDesc || !oDesc) return TECOOPS_STATUS_BAD_PARAM;
     if (!blockTable || !qData || !kCache || !vCache || !oData || !kv_seq_lens)
@@ -960,18 +1090,18 @@ extern "C" tecoopsStatus_t tecoopsFlashAttentionEx(
     for (int i = 0; i < 3; ++i)
         TECO_RETURN_IF(qDesc->dimA[i] != oDesc->dimA[i], TECOOPS_STATUS_BAD_PARAM,
                        "q and output shapes differ");
-    const int H = qDesc->dimA[1], D = qDesc->dimA[2];
+    const int total_q = qDesc->dimA[0], H = qDesc->dimA[1], D = qDesc->dimA[2];
     const int num_blocks = kDesc->dimA[0], Hkv = kDesc->dimA[1], bs = kDesc->dimA[2];
-    const int batch = btDesc->dimA[0];
+    const int batch = btDesc->dimA[0], bt_cols = btDesc->dimA[1];
     TECO_RETURN_IF(kDesc->dimA[3] != D, TECOOPS_STATUS_BAD_PARAM, "head_size mismatch");
-    TECO_RETURN_IF(D != 64 && D != 128, TECOOPS_STATUS_NOT_SUPPORTED,
-                   "flash_attention: head_size %d not supported (64, 128)", D);
+    TECO_RETURN_IF(!head_size_supported(D), TECOOPS_STATUS_NOT_SUPPORTED,
+                   "flash_attention: head_size %d not supported (32, 64, 96, 128, 160, 192)", D);
     TECO_RETURN_IF(H <= 0 || Hkv <= 0 || H % Hkv != 0, TECOOPS_STATUS_BAD_PARAM,
                    "num_heads must be a multiple of num_kv_heads");
-    TECO_RETURN_IF(bs <= 0 || num_blocks <= 0 || batch <= 0, TECOOPS_STATUS_BAD_PARAM,
-                   "empty cache or batch");
-    TECO_RETURN_IF(max_seqlen_q <= 0 || max_seqlen_k < 0, TECOOPS_STATUS_BAD_PARAM,
-                   "max_seqlen_q must be > 0 and max_seqlen_k >= 0");
+    TECO_RETURN_IF(bs <= 0 || num_blocks <= 0 || batch <= 0 || total_q < 0 || bt_cols < 0,
+                   TECOOPS_STATUS_BAD_PARAM, "empty cache or batch");
+    TECO_RETURN_IF(fixed_k_hint && max_seqlen_k <= 0, TECOOPS_STATUS_BAD_PARAM,
+                   "flash_attention: a caller workspace needs the max_seqlen_k it was sized for");
     TECO_RETURN_IF(!is_packed_rowmajor(qDesc) || !is_packed_rowmajor(oDesc) ||
                    !is_packed_rowmajor(kDesc) || !is_packed_rowmajor(vDesc) ||
                    btDesc->strideA[1] != 1,
@@ -980,7 +1110,8 @@ extern "C" tecoopsStatus_t tecoopsFlashAttentionEx(
         TECO_RETURN_IF(!tecoops::aligned(ptr, 16), TECOOPS_STATUS_BAD_PARAM,
                        "flash_attention: tensors must be 16-byte aligned");
 
-    FaParams p{};
+    FaParams &p = c.p;
+    p = FaParams{};
     p.q = static_cast<const uint16_t *>(qData);
     p.kc = static_cast<const uint16_t *>(kCache);
     p.vc = static_cast<const uint16_t *>(vCache);
@@ -997,34 +1128,90 @@ extern "C" tecoopsStatus_t tecoopsFlashAttentionEx(
     p.bs = bs;
     p.lbs = (bs & (bs - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(bs)) : -1;
     p.num_blocks = num_blocks;
+    const long long cap = static_cast<long long>(bt_cols) * bs;
+    p.kv_cap = cap > 0x7fffffffLL ? 0x7fffffff : static_cast<int>(cap);
     p.page_stride = static_cast<long long>(Hkv) * bs * D;
     const float scale = softmax_scale > 0.0f ? softmax_scale : 1.0f / std::sqrt(static_cast<float>(D));
     p.scale_log2 = scale * 1.4426950408889634f;
     p.causal = causal != 0;
 
-    const Plan pl = make_plan(batch, H, Hkv, max_seqlen_q, max_seqlen_k);
-    if (pl.decode) {
-        p.rq = pl.rq;
-        p.ncols = pl.ncols;
-        p.split_len = pl.split_len;
-        p.max_splits = pl.max_splits;
-        const size_t need = workspace_bytes(pl, batch, Hkv, D);
-        void *ws = workspace;
-        if (ws == nullptr) {
-            tecoopsStatus_t st = tecoops::handle_scratch(handle, need, &ws);
-            if (st != TECOOPS_STATUS_SUCCESS) return st;
-        }
-        const size_t per = static_cast<size_t>(batch) * Hkv * pl.max_splits * pl.ncols;
-        p.ws_o = static_cast<float *>(ws);
-        p.ws_ml = p.ws_o + per * D;
+    const int q_hint = max_seqlen_q > 0 ? max_seqlen_q : std::max(1, (total_q + batch - 1) / batch);
+    int k_hint = max_seqlen_k;
+    if (!fixed_k_hint) k_hint = max_seqlen_k > 0 ? std::min(max_seqlen_k, p.kv_cap) : p.kv_cap;
+    c.pl = make_plan(batch, H, Hkv, q_hint, k_hint);
+    c.pl.total_q = total_q;
+    if (c.pl.decode) {
+        p.rq = c.pl.rq;
+        p.ncols = c.pl.ncols;
+        p.split_len = c.pl.split_len;
+        p.max_splits = c.pl.max_splits;
+    } else {
+        p.rq = 0x7fffffff;
+    }
+    c.D = D;
+    c.bf16 = kDesc->dataType == TECOOPS_DATA_BFLOAT16;
+    return TECOOPS_STATUS_SUCCESS;
+}
+
+size_t fa_workspace_bytes(const FaCall &c) {
+    return workspace_bytes(c.pl, c.p.batch, c.p.Hkv, c.D);
+}
+
+// Enqueues the call on stream s with its split-KV partials in ws (at least
+// fa_workspace_bytes(c) bytes; unused by prefill).
+tecoopsStatus_t fa_launch(hipStream_t s, FaCall &c, void *ws) {
+    if (c.pl.decode) {
+        const size_t per = static_cast<size_t>(c.p.batch) * c.p.Hkv * c.pl.max_splits * c.pl.ncols;
+        c.p.ws_o = static_cast<float *>(ws);
+        c.p.ws_ml = c.p.ws_o + per * c.D;
     }
     using tecoops::dev::bf16;
     using tecoops::dev::f16;
-    if (kDesc->dataType == TECOOPS_DATA_BFLOAT16)
-        return D == 128 ? run<bf16, 128>(handle, p, pl, max_seqlen_q)
-                        : run<bf16, 64>(handle, p, pl, max_seqlen_q);
-    return D == 128 ? run<f16, 128>(handle, p, pl, max_seqlen_q)
-                    : run<f16, 64>(handle, p, pl, max_seqlen_q);
+    return c.bf16 ? run_d<bf16>(s, c.p, c.pl, c.D) : run_d<f16>(s, c.p, c.pl, c.D);
+}
+
+}  // namespace
+
+extern "C" tecoopsStatus_t tecoopsGetFlashAttentionWorkspaceSize(int batch, int num_heads,
+                                                                 int head_size, int max_seqlen_q,
+                                                                 int max_seqlen_k, size_t *bytes) {
+    if (bytes == nullptr || batch <= 0 || num_heads <= 0 || head_size <= 0 || max_seqlen_k <= 0)
+        return TECOOPS_STATUS_BAD_PARAM;
+    // Worst case over kv-head counts; max_seqlen_q <= 0 takes the longest q
+    // length the decode route admits (32 / G rows).
+    size_t worst = 0;
+    for (int hkv = 1; hkv <= num_heads; ++hkv) {
+        if (num_heads % hkv) continue;
+        const int G = num_heads / hkv;
+        const int q_hint = max_seqlen_q > 0 ? max_seqlen_q : std::max(1, 32 / G);
+        const Plan pl = make_plan(batch, num_heads, hkv, q_hint, max_seqlen_k);
+        const size_t b = workspace_bytes(pl, batch, hkv, head_size);
+        if (b > worst) worst = b;
+    }
+    *bytes = worst;
+    return TECOOPS_STATUS_SUCCESS;
+}
+
+extern "C" tecoopsStatus_t tecoopsFlashAttentionEx(
+    tecoopsHandle_t handle, int max_seqlen_q, int max_seqlen_k, const int *q_seq_lens,
+    const int *cu_seqlens_q, const int *kv_seq_lens, const tecoopsTensorDescriptor_t btDesc,
+    const void *blockTable, const tecoopsTensorDescriptor_t qDesc, const void *qData,
+    const tecoopsTensorDescriptor_t kDesc, const void *kCache,
+    const tecoopsTensorDescriptor_t vDesc, const void *vCache,
+    const tecoopsTensorDescriptor_t oDesc, void *oData, float softmax_scale, int causal,
+    void *workspace) {
+    FaCall c;
+    tecoopsStatus_t st = fa_prepare(handle, max_seqlen_q, max_seqlen_k, q_seq_lens, cu_seqlens_q,
+                                    kv_seq_lens, btDesc, blockTable, qDesc, qData, kDesc, kCache,
+                                    vDesc, vCache, oDesc, oData, softmax_scale, causal,
+                                    workspace != nullptr, c);
+    if (st != TECOOPS_STATUS_SUCCESS) return st;
+    void *ws = workspace;
+    if (c.pl.decode && ws == nullptr) {
+        st = tecoops::handle_scratch(handle, fa_workspace_bytes(c), &ws);
+        if (st != TECOOPS_STATUS_SUCCESS) return st;
+    }
+    return fa_launch(handle->stream, c, ws);
 }
 
 extern "C" tecoopsStatus_t tecoopsFlashAttention(
@@ -1034,10 +1221,15 @@ extern "C" tecoopsStatus_t tecoopsFlashAttention(
     const tecoopsTensorDescriptor_t kCacheDesc, const void *kCache,
     const tecoopsTensorDescriptor_t vCacheDesc, const void *vCache,
     const tecoopsTensorDescriptor_t oDataDesc, void *oData, void *workspace) {
-    (void)max_block_num;  // the reference also takes the block count from kCacheDesc
+    // The reference accepts workspace and never reads it
+    // (flash_attention.cpp:110), and takes the block count from kCacheDesc:
+    // both are ignored here too, so a caller's unrelated buffer is never
+    // written.  The split-KV partials live in the handle's scratch.
+    (void)max_block_num;
+    (void)workspace;
     if (q_seq_lens == nullptr) return handle ? TECOOPS_STATUS_BAD_PARAM : TECOOPS_STATUS_NOT_INITIALIZED;
     return tecoopsFlashAttentionEx(handle, max_seqlen_q, max_seqlen_k, q_seq_lens, nullptr,
                                    kv_seq_lens, blockTableDesc, blockTable, qDataDesc, qData,
                                    kCacheDesc, kCache, vCacheDesc, vCache, oDataDesc, oData,
-                                   -1.0f, 1, workspace);
+                                   -1.0f, 1, nullptr);
 }

@@ -3,8 +3,9 @@
 // Behaviour follows teco/interface/common/tecoops.cpp:38-258: the same
 // NULL-argument statuses, the same row-major default strides in
 // SetTensorNdDescriptor and the same format-to-stride table in
-// SetTensor4dDescriptor.  Differences: the handle owns a scratch buffer and
-// descriptors free their >8-dim arrays.  Create/Destroy of a handle that never
+// SetTensor4dDescriptor.  Differences: the handle owns a scratch buffer per
+// stream it runs split-KV attention on, and descriptors free their >8-dim
+// arrays.  Create/Destroy of a handle that never
 // ran an op make no HIP call.
 #include "common.h"
 
@@ -23,11 +24,10 @@ tecoopsStatus_t tecoopsCreate(tecoopsHandle_t *handle) {
 
 tecoopsStatus_t tecoopsDestroy(tecoopsHandle_t handle) {
     if (handle == nullptr) return TECOOPS_STATUS_BAD_PARAM;
-    if (handle->scratch != nullptr) {
-        // Work enqueued on the handle's stream may still read the scratch.
-        (void)hipStreamSynchronize(handle->stream);
-        (void)hipFree(handle->scratch);
-    }
+    // hipFree synchronises the device first: enqueued work that still reads
+    // a buffer finishes before it is freed.
+    for (ScratchSlot &sl : handle->scratch)
+        if (sl.ptr != nullptr) (void)hipFree(sl.ptr);
     delete handle;
     return TECOOPS_STATUS_SUCCESS;
 }
@@ -190,26 +190,41 @@ namespace tecoops {
 
 tecoopsStatus_t handle_scratch(tecoopsHandle_t handle, size_t bytes, void **out) {
     if (bytes == 0) bytes = 256;
-    if (handle->scratch_bytes < bytes) {
-        if (handle->scratch != nullptr) {
-            if (hipStreamSynchronize(handle->stream) != hipSuccess ||
-                hipFree(handle->scratch) != hipSuccess) {
-                handle->scratch = nullptr;
-                handle->scratch_bytes = 0;
-                return TECOOPS_STATUS_INTERNAL_ERROR;
+    ScratchSlot *slot = nullptr;
+    for (ScratchSlot &sl : handle->scratch)
+        if (sl.ptr != nullptr && sl.stream == handle->stream) slot = &sl;
+    if (slot == nullptr) {  // a free slot, else the least recently used one
+        slot = &handle->scratch[0];
+        for (ScratchSlot &sl : handle->scratch) {
+            if (sl.ptr == nullptr) {
+                slot = &sl;
+                break;
             }
-            handle->scratch = nullptr;
-            handle->scratch_bytes = 0;
+            if (sl.last_use < slot->last_use) slot = &sl;
         }
-        size_t grow = bytes + bytes / 4;
-        if (hipMalloc(&handle->scratch, grow) != hipSuccess) {
+        slot->stream = handle->stream;
+    }
+    if (slot->bytes < bytes) {
+        // hipFree synchronises the device, so work still reading the old
+        // buffer (on this slot's stream) has finished.
+        if (slot->ptr != nullptr && hipFree(slot->ptr) != hipSuccess) {
             (void)hipGetLastError();
-            handle->scratch = nullptr;
+            *slot = ScratchSlot{};
+            return TECOOPS_STATUS_INTERNAL_ERROR;
+        }
+        *slot = ScratchSlot{};
+        const size_t grow = bytes + bytes / 4;
+        void *p = nullptr;
+        if (hipMalloc(&p, grow) != hipSuccess) {
+            (void)hipGetLastError();
             return TECOOPS_STATUS_ALLOC_FAILED;
         }
-        handle->scratch_bytes = grow;
+        slot->stream = handle->stream;
+        slot->ptr = p;
+        slot->bytes = grow;
     }
-    *out = handle->scratch;
+    slot->last_use = ++handle->uses;
+    *out = slot->ptr;
     return TECOOPS_STATUS_SUCCESS;
 }
 

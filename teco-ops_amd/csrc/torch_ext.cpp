@@ -65,6 +65,18 @@ void need_cuda(std::initializer_list<const Tensor *> ts) {
         if (t && t->defined()) TORCH_CHECK(t->is_cuda(), "tecoops: tensors must be on the GPU");
 }
 
+// The C ABI takes plain pointers with packed row-major extents.
+void need_contiguous(std::initializer_list<const Tensor *> ts) {
+    for (const Tensor *t : ts)
+        if (t && t->defined())
+            TORCH_CHECK(t->is_contiguous(), "tecoops: tensors must be contiguous");
+}
+
+void need_dtype(const Tensor &t, at::ScalarType st, const char *name) {
+    TORCH_CHECK(t.scalar_type() == st, "tecoops: ", name, " must be ", st, ", got ",
+                t.scalar_type());
+}
+
 struct Desc {
     tecoopsTensorDescriptor_t d = nullptr;
     Desc(const Tensor &t, tecoopsDataType_t dt) {
@@ -84,7 +96,13 @@ struct Desc {
 void reshape_and_cache(const Tensor &key, const Tensor &value, const Tensor &slot_mapping,
                        Tensor &key_cache, Tensor &value_cache) {
     need_cuda({&key, &value, &slot_mapping, &key_cache, &value_cache});
+    need_contiguous({&key, &value, &slot_mapping, &key_cache, &value_cache});
     TORCH_CHECK(slot_mapping.scalar_type() == at::kLong, "slot_mapping must be int64");
+    TORCH_CHECK(key.dim() == 3 && key_cache.dim() == 4 && value.sizes() == key.sizes() &&
+                    value_cache.sizes() == key_cache.sizes() &&
+                    slot_mapping.numel() == key.size(0),
+                "reshape_and_cache: key/value [T, Hkv, D], caches [blocks, Hkv, bs, D], "
+                "slot_mapping [T]");
     check(tecoopsReshapeAndCacheEx(handle_for(key), key.data_ptr(), value.data_ptr(),
                                    slot_mapping.data_ptr<int64_t>(), key_cache.data_ptr(),
                                    value_cache.data_ptr(), key.size(0), key.size(1), key.size(2),
@@ -96,10 +114,25 @@ void reshape_and_cache(const Tensor &key, const Tensor &value, const Tensor &slo
 void rms_norm(const Tensor &input, const Tensor &weight, const c10::optional<Tensor> &residual,
               Tensor &output, const c10::optional<Tensor> &residual_out, double eps) {
     need_cuda({&input, &weight, &output});
-    const void *r = residual.has_value() ? residual->data_ptr() : nullptr;
-    void *ro = residual_out.has_value() ? residual_out->data_ptr() : nullptr;
-    check(tecoopsRmsNormEx(handle_for(input), input.data_ptr(), weight.data_ptr(), r,
-                           output.data_ptr(), ro, input.size(0), input.size(1),
+    const Tensor *res = residual.has_value() ? &*residual : nullptr;
+    const Tensor *res_out = residual_out.has_value() ? &*residual_out : nullptr;
+    need_contiguous({&input, &weight, &output, res, res_out});
+    // leading dimensions are rows, as in the plugin
+    const int64_t D = input.size(-1);
+    const int64_t N = D ? input.numel() / D : 0;
+    const at::ScalarType st = input.scalar_type();
+    need_dtype(weight, st, "weight");
+    need_dtype(output, st, "output");
+    TORCH_CHECK(weight.numel() == D && output.numel() == input.numel(),
+                "rms_norm: weight must hold hidden_size elements and output match input");
+    for (const Tensor *t : {res, res_out})
+        if (t) {
+            need_dtype(*t, st, "residual");
+            TORCH_CHECK(t->numel() == input.numel(), "rms_norm: residual tensors must match input");
+        }
+    check(tecoopsRmsNormEx(handle_for(input), input.data_ptr(), weight.data_ptr(),
+                           res ? res->data_ptr() : nullptr, output.data_ptr(),
+                           res_out ? res_out->data_ptr() : nullptr, N, D,
                            static_cast<float>(eps), dtype_of(input)),
           "rms_norm");
 }
@@ -207,7 +240,13 @@ void rotary_reshape_and_cache(const Tensor &positions, Tensor &query, Tensor &ke
 
 void gemv(const Tensor &weight, const Tensor &x, Tensor &out) {
     need_cuda({&weight, &x, &out});
+    need_contiguous({&weight, &x, &out});
+    need_dtype(weight, x.scalar_type(), "weight");
+    need_dtype(out, x.scalar_type(), "out");
     const int B = x.dim() == 2 ? x.size(0) : 1;
+    TORCH_CHECK(weight.dim() == 2 && x.size(-1) == weight.size(1) &&
+                    out.numel() == B * weight.size(0),
+                "gemv: weight [N, K], x [B, K], out [B, N]");
     check(tecoopsGemv(handle_for(x), weight.data_ptr(), x.data_ptr(), out.data_ptr(), B,
                       weight.size(0), weight.size(1), dtype_of(x)),
           "gemv");
@@ -215,7 +254,15 @@ void gemv(const Tensor &weight, const Tensor &x, Tensor &out) {
 
 void gemv_int8(const Tensor &weight, const Tensor &scales, const Tensor &x, Tensor &out) {
     need_cuda({&weight, &scales, &x, &out});
+    need_contiguous({&weight, &scales, &x, &out});
+    need_dtype(weight, at::kChar, "weight");
+    need_dtype(scales, at::kHalf, "scales");
+    need_dtype(x, at::kHalf, "x");
+    need_dtype(out, at::kHalf, "out");
     const int B = x.dim() == 2 ? x.size(0) : 1;
+    TORCH_CHECK(weight.dim() == 2 && x.size(-1) == weight.size(1) &&
+                    out.numel() == B * weight.size(0) && scales.numel() == weight.size(0),
+                "gemv_int8: weight [N, K], scales [N], x [B, K], out [B, N]");
     check(tecoopsGemvInt8(handle_for(x), weight.data_ptr<int8_t>(), scales.data_ptr(),
                           x.data_ptr(), out.data_ptr(), B, weight.size(0), weight.size(1)),
           "gemv_int8");

@@ -18,6 +18,7 @@ Differences from the reference wrappers, all toward its documented intent:
 """
 import ctypes
 import os
+import sys
 import threading
 
 import torch
@@ -43,28 +44,45 @@ __all__ = [
     "memset", "ops",
 ]
 
-_handles = {}   # device index -> [handle, bound stream]
-_lock = threading.Lock()
+_tls = threading.local()   # per thread: {device index: _Handle}
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
+class _Handle:
+    """One tecoops handle of one (thread, device), bound to that thread's
+    current torch stream of the device.  Threads never share a handle, so a
+    thread cannot enqueue on another thread's stream, and the handle orders
+    its split-KV scratch across the streams it is used on."""
+
+    def __init__(self):
+        self.h = ctypes.c_void_p()
+        _lib.call("tecoopsCreate", ctypes.byref(self.h))
+        self.stream = None
+
+    def __del__(self):
+        # the thread ended: its handle (and scratch) go with it
+        try:
+            if self.h and not sys.is_finalizing():
+                _lib.lib().tecoopsDestroy(self.h)
+        except Exception:
+            pass
+
+
 def _handle(device):
-    """Per-device handle bound to the device's current torch stream (rebound
-    only when the current stream changes)."""
+    """The calling thread's handle for `device`, bound to the thread's current
+    torch stream there (rebound only when that stream changes)."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    entry = _handles.get(idx)
+    handles = getattr(_tls, "handles", None)
+    if handles is None:
+        handles = _tls.handles = {}
+    entry = handles.get(idx)
     if entry is None:
-        with _lock:
-            entry = _handles.get(idx)
-            if entry is None:
-                h = ctypes.c_void_p()
-                _lib.call("tecoopsCreate", ctypes.byref(h))
-                entry = _handles[idx] = [h, None]
+        entry = handles[idx] = _Handle()
     stream = _raw_stream(idx) if _raw_stream else torch.cuda.current_stream(idx).cuda_stream
-    if stream != entry[1]:
-        _lib.call("tecoopsSetStream", entry[0], ctypes.c_void_p(stream))
-        entry[1] = stream
-    return entry[0]
+    if stream != entry.stream:
+        _lib.call("tecoopsSetStream", entry.h, ctypes.c_void_p(stream))
+        entry.stream = stream
+    return entry.h
 
 
 def _dtype_code(t):
@@ -83,6 +101,19 @@ def _check_cuda(*ts):
     for t in ts:
         if t is not None and not t.is_cuda:
             raise ValueError("tecoops: tensors must live on a cuda (ROCm) device")
+
+
+def _check_contiguous(**ts):
+    """The C ABI takes plain pointers with packed row-major extents."""
+    for name, t in ts.items():
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"tecoops: {name} must be contiguous")
+
+
+def _check_dtype(t, name, *dtypes):
+    if t is not None and t.dtype not in dtypes:
+        raise TypeError(f"tecoops: {name} must be {' or '.join(str(d) for d in dtypes)}, "
+                        f"got {t.dtype}")
 
 
 class _Desc:
@@ -118,6 +149,8 @@ def reshape_and_cache(key, value, slot_mapping, key_cache, value_cache):
     """key/value [T, Hkv, D]; caches [num_blocks, Hkv, block_size, D];
     slot_mapping int64 [T] (reference torch_ext.cpp:61-79)."""
     _check_cuda(key, value, slot_mapping, key_cache, value_cache)
+    _check_contiguous(key=key, value=value, slot_mapping=slot_mapping, key_cache=key_cache,
+                      value_cache=value_cache)
     if slot_mapping.dtype != torch.int64:
         raise TypeError("slot_mapping must be int64")
     T, H, D = key.shape
@@ -129,7 +162,19 @@ def reshape_and_cache(key, value, slot_mapping, key_cache, value_cache):
 def rms_norm(input, weight, residual, output, residual_out, eps):
     """(reference torch_ext.cpp:81-97)."""
     _check_cuda(input, weight, residual, output, residual_out)
-    N, D = input.shape
+    _check_contiguous(input=input, weight=weight, residual=residual, output=output,
+                      residual_out=residual_out)
+    D = input.shape[-1]
+    N = input.numel() // D if D else 0      # leading dims are rows, as in the plugin
+    for name, t in (("weight", weight), ("residual", residual), ("output", output),
+                    ("residual_out", residual_out)):
+        _check_dtype(t, name, input.dtype)
+    if weight.numel() != D or output.numel() != input.numel():
+        raise ValueError("tecoops.rms_norm: weight must hold hidden_size elements and output "
+                         "match input")
+    for name, t in (("residual", residual), ("residual_out", residual_out)):
+        if t is not None and t.numel() != input.numel():
+            raise ValueError(f"tecoops.rms_norm: {name} must match input")
     _lib.call("tecoopsRmsNormEx", _handle(input.device), _ptr(input), _ptr(weight),
               _ptr(residual), _ptr(output), _ptr(residual_out), N, D, float(eps),
               _dtype_code(input))
@@ -234,8 +279,13 @@ def rotary_reshape_and_cache(positions, query, key, value, slot_mapping, key_cac
 def gemv(weight, x, out):
     """out[b, n] = sum_k weight[n, k] x[b, k]; weight [N, K], x [B, K], out [B, N]."""
     _check_cuda(weight, x, out)
+    _check_contiguous(weight=weight, x=x, out=out)
+    _check_dtype(weight, "weight", x.dtype)
+    _check_dtype(out, "out", x.dtype)
     N, K = weight.shape
     B = x.shape[0] if x.dim() == 2 else 1
+    if x.shape[-1] != K or out.numel() != B * N:
+        raise ValueError(f"tecoops.gemv: x must be [B, {K}] and out [B, {N}]")
     _lib.call("tecoopsGemv", _handle(x.device), _ptr(weight), _ptr(x), _ptr(out), B, N, K,
               _dtype_code(x))
 
@@ -243,8 +293,15 @@ def gemv(weight, x, out):
 def gemv_int8(weight, scales, x, out):
     """out[b, n] = scales[n] * sum_k weight[n, k] x[b, k]; weight int8 [N, K]."""
     _check_cuda(weight, scales, x, out)
+    _check_contiguous(weight=weight, scales=scales, x=x, out=out)
+    _check_dtype(weight, "weight", torch.int8)
+    _check_dtype(scales, "scales", torch.float16)
+    _check_dtype(x, "x", torch.float16)
+    _check_dtype(out, "out", torch.float16)
     N, K = weight.shape
     B = x.shape[0] if x.dim() == 2 else 1
+    if x.shape[-1] != K or out.numel() != B * N or scales.numel() != N:
+        raise ValueError(f"tecoops.gemv_int8: x must be [B, {K}], out [B, {N}], scales [{N}]")
     _lib.call("tecoopsGemvInt8", _handle(x.device), _ptr(weight), _ptr(scales), _ptr(x),
               _ptr(out), B, N, K)
 

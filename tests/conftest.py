@@ -29,3 +29,15 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+# Parity figures (max abs error, DIFF1, ...) that tests record with
+# helpers.record(); printed after the run, also under -q.
+FIGURES = []
+
+
+def pytest_terminal_summary(terminalreporter):
+    if FIGURES:
+        terminalreporter.section("parity figures")
+        for line in FIGURES:
+            terminalreporter.write_line(line)

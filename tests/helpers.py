@@ -65,3 +65,10 @@ def diff3_max(got, ref):
     d = np.abs(got - ref)
     rel = np.where(np.abs(ref) < 1e-4, d, d / np.maximum(np.abs(ref), 1e-30))
     return float(rel.max()) if rel.size else 0.0
+
+
+def record(line):
+    """Prints a parity figure now and lists it again in the run's summary."""
+    import conftest
+    print(line, flush=True)
+    conftest.FIGURES.append(line)

@@ -172,8 +172,8 @@ def test_flash_attention_validation(handle):
     vbf = _desc(_lib.DATA_BFLOAT16, [16, 2, 16, 128])
     kbf = _desc(_lib.DATA_BFLOAT16, [16, 2, 16, 128])
     vshape = _desc(_lib.DATA_HALF, [16, 2, 32, 128])
-    q96 = _desc(_lib.DATA_HALF, [8, 4, 96])
-    k96 = _desc(_lib.DATA_HALF, [16, 2, 16, 96])
+    q80 = _desc(_lib.DATA_HALF, [8, 4, 80])
+    k80 = _desc(_lib.DATA_HALF, [16, 2, 16, 80])
     f = L.tecoopsFlashAttention
 
     def call(h=handle, kd=k, vd=v, qd=q, od=o):
@@ -184,9 +184,15 @@ def test_flash_attention_validation(handle):
     assert call(kd=vf, vd=vf) == BAD      # neither half nor bf16
     assert call(kd=kbf, vd=vbf) == BAD    # q/o stay half: types must agree
     assert call(vd=vshape) == BAD         # k/v shape mismatch (:62-67)
-    assert call(qd=q96, od=q96, kd=k96, vd=k96) == NOT_SUP
-    assert f(handle, 0, 16, 16, P, P, bt, P, q, P, k, P, v, P, o, P, None) == BAD
-    for d in (bt, q, k, v, o, vf, vbf, kbf, vshape, q96, k96):
+    # head sizes: multiples of 32 up to 192 (flash_attention.scpp:188, :347-348)
+    assert call(qd=q80, od=q80, kd=k80, vd=k80) == NOT_SUP
+    # max_seqlen_q / max_seqlen_k are launch hints (the reference never reads
+    # them), but a caller workspace is sized by max_seqlen_k, so the Ex entry
+    # point needs it positive when one is passed
+    ex = L.tecoopsFlashAttentionEx
+    assert ex(handle, 1, 0, P, None, P, bt, P, q, P, k, P, v, P, o, P, -1.0, 1, P) == BAD
+    assert ex(handle, 1, 16, None, None, P, bt, P, q, P, k, P, v, P, o, P, -1.0, 1, P) == BAD
+    for d in (bt, q, k, v, o, vf, vbf, kbf, vshape, q80, k80):
         L.tecoopsDestroyTensorDescriptor(d)
 
 
@@ -205,4 +211,29 @@ def test_rotary_and_gemv_validation(handle):
     ws = ctypes.c_size_t()
     assert L.tecoopsGetFlashAttentionWorkspaceSize(64, 32, 128, 1, 8192, ctypes.byref(ws)) == OK
     assert ws.value > 0
-    assert L.tecoopsGetFlashAttentionWorkspaceSize(64, 32, 128, 0, 8192, ctypes.byref(ws)) == BAD
+    # max_seqlen_q <= 0 sizes for the longest q the decode route takes
+    big = ctypes.c_size_t()
+    assert L.tecoopsGetFlashAttentionWorkspaceSize(64, 32, 128, 0, 8192, ctypes.byref(big)) == OK
+    assert big.value >= ws.value
+    assert L.tecoopsGetFlashAttentionWorkspaceSize(64, 32, 128, 1, 0, ctypes.byref(ws)) == BAD
+
+
+def test_reference_artefact_names():
+    """The reference's library names (teco/CMakeLists.txt:99-129) load this
+    build's libraries and export the tecoops.h / plugin entry points."""
+    d = os.path.dirname(_lib.LIB_PATH)
+    for name in ("libteco_ops.so", "libteco_ops_plugin.so"):
+        L = ctypes.CDLL(os.path.join(d, name))
+        for f in header_functions():
+            assert getattr(L, f) is not None, (name, f)
+    P_ = ctypes.CDLL(os.path.join(d, "libTecoInferPlugin.so"))
+    assert P_.tecoopsPluginCreate is not None
+
+
+def test_torch_ext_module_names():
+    """The reference package's extension module (api/tecoops/__init__.py:3)."""
+    from tecoops import _torch_ext
+    for name in ("flatten_rays", "morton3D_invert", "reshape_and_cache", "rms_norm",
+                 "flash_attn_varlen_func", "causal_conv1d_fn_torch"):
+        assert callable(getattr(_torch_ext, name))
+    from tecoops._torch_ext import rms_norm  # noqa: F401

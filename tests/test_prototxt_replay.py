@@ -32,7 +32,7 @@ from tecoops import _lib
 from oracle import harness
 from oracle import oracle as orc
 
-from helpers import as_f32, assert_close, dev, diff3_max, host_bits
+from helpers import as_f32, assert_close, dev, diff3_max, host_bits, record
 
 pytestmark = pytest.mark.gpu
 
@@ -58,7 +58,7 @@ def outputs(case):
 
 
 def report(case, **vals):
-    print(case["file"], " ".join(f"{k}={v:.3e}" for k, v in vals.items()), flush=True)
+    record(case["file"] + " " + " ".join(f"{k}={v:.3e}" for k, v in vals.items()))
 
 
 @pytest.mark.parametrize("i", range(len(CASES["rms_norm"])))
