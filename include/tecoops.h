@@ -236,6 +236,30 @@ tecoopsStatus_t tecoopsFlashAttentionEx(tecoopsHandle_t handle,
                                         void *oData, float softmax_scale, int causal,
                                         void *workspace);
 
+/* Flash attention that allocates nothing, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  Arguments and
+ * results are those of tecoopsFlashAttentionEx without a workspace: the
+ * split-KV partials of decode go to a static device array of 64 MiB per GPU
+ * (held until the process ends) instead of the handle's scratch, and a call
+ * whose decode plan needs more returns TECOOPS_STATUS_BAD_PARAM.  Every call
+ * on a GPU shares that array: calls that overlap on one GPU (different
+ * streams, threads or handles) race and must be ordered by the caller. */
+tecoopsStatus_t tecoopsFlashAttentionNoAlloc(tecoopsHandle_t handle,
+                                             int max_seqlen_q, int max_seqlen_k,
+                                             const int *q_seq_lens, const int *cu_seqlens_q,
+                                             const int *kv_seq_lens,
+                                             const tecoopsTensorDescriptor_t blockTableDesc,
+                                             const void *blockTable,
+                                             const tecoopsTensorDescriptor_t qDataDesc,
+                                             const void *qData,
+                                             const tecoopsTensorDescriptor_t kCacheDesc,
+                                             const void *kCache,
+                                             const tecoopsTensorDescriptor_t vCacheDesc,
+                                             const void *vCache,
+                                             const tecoopsTensorDescriptor_t oDataDesc,
+                                             void *oData, float softmax_scale, int causal);
+
 /* Bytes of caller workspace tecoopsFlashAttentionEx needs for these sizes
  * (max_seqlen_k > 0; max_seqlen_q <= 0 sizes for the longest q length the
  * split-KV decode route takes). */

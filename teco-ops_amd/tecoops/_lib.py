@@ -64,6 +64,7 @@ SIGNATURES = {
     "tecoopsRmsNormEx": (I, [P, P, P, P, P, P, I, I, F, I]),
     "tecoopsReshapeAndCacheEx": (I, [P, P, P, P, P, P, I, I, I, I, I, I]),
     "tecoopsFlashAttentionEx": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, F, I, P]),
+    "tecoopsFlashAttentionNoAlloc": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, F, I]),
     "tecoopsGetFlashAttentionWorkspaceSize": (I, [I, I, I, I, I, P]),
     "tecoopsCausalConv1dEx": (I, [P, I, I, I, I, P, LL, LL, LL, P, LL, LL, LL, P, I, I, P, P, I,
                                   P, P, P, I, I, I]),
