@@ -7,6 +7,9 @@ inputs already resident in HBM (synthetic seeded data):
   rms_norm        x fp16 [4096, 4096], eps 1e-6
   reshape_cache   key/value fp16 [8192, 8, 128] -> 1024 blocks x 16 slots
   causal_conv1d   x fp16 [8, 4096, 2048], width 4, bias, SiLU, final state
+  causal_conv1d_tm  the same shape in the reference C layout: x [8 x 2048
+                  tokens, 4096] token-major through causal_conv1d_fn_torch
+                  (query_start_loc, weight [4, 4096], no bias), final state
   rotary          q [8192, 32, 128], k [8192, 8, 128], neox, base 1e4
   rotary_cache    the fused decode step: rotary on q, k [8192, 8, 128] and
                   k, v into 1024 blocks x 16 (rotary + reshape_and_cache)
@@ -21,7 +24,9 @@ this steady state an op's HBM traffic per launch equals its algorithmic bytes
 time: K back-to-back launches of the op between one pair of torch.cuda events
 on the stream the ops are enqueued on (tecoops binds the current torch
 stream), divided by K, right after a warm-up of at least W launches and 30 ms
-of the same op.
+of the same op.  Beside it, `us_median20` is the median of 20 more launches
+of the op, each between its own pair of events (the extra event markers
+between launches can add a little to each).
 
 Prints ONE JSON line.  `value` is flash-attention prefill TFLOP/s (causal
 FLOP count / average kernel time), the throughput figure of BASELINE.json's
@@ -124,7 +129,7 @@ def build_ops(names=None):
         for _ in range(copies_for(ws)):
             x = seeded_bits(rng, (4096, 4096))
             y = torch.empty_like(x)
-            fns.append(lambda x=x, y=y: tecoops.rms_norm(x, w, None, y, None, 1e-6))
+            fns.append(lambda x=x, y=y, w=w: tecoops.rms_norm(x, w, None, y, None, 1e-6))
         ops["rms_norm"] = (fns, dict(bytes=2 * 4096 * 4096 * 2 + 4096 * 2))
 
     if want("reshape_and_cache"):
@@ -139,7 +144,7 @@ def build_ops(names=None):
             val = seeded_bits(rng, (T, Hkv, D))
             kc = torch.zeros((NB, Hkv, BS, D), dtype=torch.float16, device="cuda")
             vc = torch.zeros_like(kc)
-            fns.append(lambda key=key, val=val, kc=kc, vc=vc:
+            fns.append(lambda key=key, val=val, kc=kc, vc=vc, slots=slots:
                        tecoops.reshape_and_cache(key, val, slots, kc, vc))
         ops["reshape_and_cache"] = (fns, dict(bytes=4 * T * Hkv * D * 2 + T * 8))
 
@@ -155,9 +160,29 @@ def build_ops(names=None):
             cx = seeded_bits(rng, (B, C, L))
             co = torch.empty_like(cx)
             cst = torch.zeros((B, 3, C), dtype=torch.float16, device="cuda")
-            fns.append(lambda cx=cx, co=co, cst=cst: tecoops.causal_conv1d(cx, cw, cb, co,
-                                                                             conv_states=cst))
+            fns.append(lambda cx=cx, co=co, cst=cst, cw=cw, cb=cb: tecoops.causal_conv1d(
+                cx, cw, cb, co, conv_states=cst))
         ops["causal_conv1d"] = (fns, dict(bytes=2 * B * C * L * 2 + C * 4 * 2 + C * 2 + B * 3 * C * 2))
+
+    if want("causal_conv1d_tm"):
+        rng = np.random.default_rng(1009)  # each op has its own seed
+        # the BASELINE conv shape in the reference C layout [tokens, dim]
+        B, C, L = 8, 4096, 2048
+        T = B * L
+        ws = 2 * T * C * 2
+        cw = seeded_bits(rng, (4, C), scale=0.5)             # [width, dim]
+        qsl = torch.arange(0, T + 1, L, dtype=torch.int32, device="cuda")
+        cidx = torch.arange(B, dtype=torch.int32, device="cuda")
+        hinit = torch.zeros(B, dtype=torch.int8, device="cuda")
+        fns = []
+        for _ in range(copies_for(ws)):
+            cx = seeded_bits(rng, (T, C))                    # token-major storage
+            co = torch.empty_like(cx)
+            cst = torch.zeros((B, 3, C), dtype=torch.float16, device="cuda")
+            fns.append(lambda cx=cx, co=co, cst=cst, cw=cw, qsl=qsl, cidx=cidx, hinit=hinit:
+                       tecoops.causal_conv1d_fn_torch(co.t(), cst, cx.t(), cw, qsl, cidx, hinit,
+                                                      -1))
+        ops["causal_conv1d_tm"] = (fns, dict(bytes=2 * T * C * 2 + 4 * C * 2 + B * 3 * C * 2))
 
     if want("rotary"):
         rng = np.random.default_rng(1004)  # each op has its own seed
@@ -168,7 +193,7 @@ def build_ops(names=None):
         for _ in range(copies_for(ws)):
             q = seeded_bits(rng, (8192, 32, 128))
             k = seeded_bits(rng, (8192, 8, 128))
-            fns.append(lambda q=q, k=k: tecoops.rotary_embedding(pos, q, k, 128))
+            fns.append(lambda q=q, k=k, pos=pos: tecoops.rotary_embedding(pos, q, k, 128))
         ops["rotary"] = (fns, dict(bytes=2 * (8192 * 40 * 128) * 2 + 8192 * 8))
 
     if want("rotary_cache"):
@@ -186,8 +211,8 @@ def build_ops(names=None):
             v = seeded_bits(rng, (T, Hkv, D))
             kc = torch.zeros((NB, Hkv, BS, D), dtype=torch.float16, device="cuda")
             vc = torch.zeros_like(kc)
-            fns.append(lambda q=q, k=k, v=v, kc=kc, vc=vc: tecoops.rotary_reshape_and_cache(
-                pos, q, k, v, slots, kc, vc, D))
+            fns.append(lambda q=q, k=k, v=v, kc=kc, vc=vc, pos=pos, slots=slots:
+                       tecoops.rotary_reshape_and_cache(pos, q, k, v, slots, kc, vc, D))
         ops["rotary_cache"] = (fns, dict(bytes=ws + 2 * T * 8))
 
     if want("gemv_f16_b1", "gemv_f16_b8", "gemv_i8_b1", "gemv_i8_b8"):
@@ -211,17 +236,21 @@ def build_ops(names=None):
         rng = np.random.default_rng(1007)  # each op has its own seed
         # flash attention prefill: identity block tables over 4 x 256 blocks
         nbp = FA_S // 16
-        fq = seeded_bits(rng, (FA_B * FA_S, FA_H, FA_D), dtype="bf16")
-        fk = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
-        fv = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
-        fo = torch.empty_like(fq)
         bt = torch.arange(FA_B * nbp, dtype=torch.int32, device="cuda").view(FA_B, nbp)
         cu = torch.arange(0, FA_B + 1, dtype=torch.int32, device="cuda") * FA_S
         sk = torch.full((FA_B,), FA_S, dtype=torch.int32, device="cuda")
-        ops["fa_prefill"] = (
-            [lambda: tecoops.flash_attn_varlen_func(fq, fk, fv, FA_S, cu, FA_S, None, sk, scale, True,
-                                                    None, bt, False, fo)],
-            dict(flops=FA_PREFILL_FLOP, bytes=(fq.numel() * 2 + fk.numel() * 2) * 2))
+        q_bytes = FA_B * FA_S * FA_H * FA_D * 2
+        kv_bytes = 2 * FA_B * FA_S * FA_HKV * FA_D * 2
+        fns = []
+        for _ in range(copies_for(2 * q_bytes + kv_bytes)):
+            fq = seeded_bits(rng, (FA_B * FA_S, FA_H, FA_D), dtype="bf16")
+            fk = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
+            fv = seeded_bits(rng, (FA_B * nbp, FA_HKV, 16, FA_D), dtype="bf16")
+            fo = torch.empty_like(fq)
+            fns.append(lambda fq=fq, fk=fk, fv=fv, fo=fo, cu=cu, sk=sk, bt=bt:
+                       tecoops.flash_attn_varlen_func(fq, fk, fv, FA_S, cu, FA_S, None, sk, scale,
+                                                      True, None, bt, False, fo))
+        ops["fa_prefill"] = (fns, dict(flops=FA_PREFILL_FLOP, bytes=2 * q_bytes + kv_bytes))
 
     if want("fa_decode"):
         rng = np.random.default_rng(1008)  # each op has its own seed
@@ -430,6 +459,7 @@ def main():
     # events on the stream they are enqueued on, so the average per launch
     # excludes host overhead.
     ev = {}
+    med = {}
     wall = 0.0
     for n, (fns, _) in ops.items():
         i, t_w = 0, time.perf_counter()
@@ -452,11 +482,20 @@ def main():
         torch.cuda.synchronize()
         wall += time.perf_counter() - t0
         ev[n] = (a, b)
+        # 20 more launches, each between its own pair of events: the median
+        i += args.steps
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(21)]
+        marks[0].record()
+        for j in range(20):
+            fns[(i + j) % len(fns)]()
+            marks[j + 1].record()
+        torch.cuda.synchronize()
+        med[n] = float(np.median([marks[j].elapsed_time(marks[j + 1]) for j in range(20)])) * 1e3
 
     report = {}
     for n, (fns, work) in ops.items():
         us = 1e3 * ev[n][0].elapsed_time(ev[n][1]) / args.steps
-        r = {"us": round(us, 3), "rotating_copies": len(fns)}
+        r = {"us": round(us, 3), "us_median20": round(med[n], 3), "rotating_copies": len(fns)}
         if "flops" in work and n == "fa_prefill":
             tf = work["flops"] / (us * 1e-6) / 1e12
             r.update(tflops=round(tf, 2), frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4), bound="mfma")

@@ -11,16 +11,19 @@
 //   conv_state[c] = last W-1 entries of full_x.
 // act is SiLU (v / (1 + exp(-v))); the reference always applies it.
 //
-// gfx950 design: every lane owns one channel d of one sequence and a chunk of
-// consecutive tokens held in registers with the W-1 inputs before it (a
-// sliding window), so each input is fetched from HBM once.  Two mappings:
+// gfx950 design: every lane holds a chunk of consecutive tokens in registers
+// with the W-1 inputs before it (a sliding window), so each input is fetched
+// from HBM once.  Three mappings:
 //   token stride 1 (e.g. [batch, dim, seqlen], the reference's [dim, tokens]):
 //     a wave streams whole rows, lanes on consecutive 8-token chunks ->
 //     16-byte loads / stores, the W-1 overlap passed between lanes in
 //     registers (conv1d_rows_kernel);
-//   otherwise (e.g. [tokens, dim]): consecutive lanes take consecutive
-//     channels of one 16-token chunk -> coalesced 2-byte accesses, the overlap
-//     re-read through L1/L2 (conv1d_kernel).
+//   channel stride 1 with dim % 8 == 0 (the reference C layout [tokens, dim]):
+//     a lane owns 8 consecutive channels (one 16-byte vector per token) of a
+//     16-token chunk of the global token axis; the W-1 rows before the chunk
+//     are re-read from L2 (conv1d_tokens_kernel);
+//   otherwise: consecutive lanes take consecutive channels of one 16-token
+//     chunk with 2-byte accesses (conv1d_kernel).
 // Only one lane of a (sequence, channel) touches conv_state, reading the old
 // state before writing the new one, so there is no cross-lane race.
 // HBM-bound: algorithmic bytes = 2 * (x + out) + weights + bias + state.
@@ -50,14 +53,26 @@ struct ConvArgs {
 };
 
 // SiLU v / (1 + e^-v) with the hardware exp2 and reciprocal (about 1 ulp
-// each); saturates correctly to 0 / v for large |v|.
-__device__ __forceinline__ float act(float v, int silu) {
-    if (!silu) return v;
+// each); saturates correctly to 0 / v for large |v|.  A template flag, so
+// the kernels carry no per-element select for it.  (Folding -log2(e) into
+// the weights saves one multiply per element but measured no faster: these
+// kernels wait on memory, not on the VALU.)
+template <bool SILU>
+__device__ __forceinline__ float act(float v) {
+    if (!SILU) return v;
     const float e = __builtin_amdgcn_exp2f(-v * 1.4426950408889634f);
     return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-template <int W, bool SEQ_CONTIG, int CH>
+// Two floats rounded to fp16 (round to nearest even) and packed, as one
+// packed conversion.
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
+}
+
+template <int W, bool SEQ_CONTIG, int CH, bool SILU>
 __device__ __forceinline__ void conv1d_body(const ConvArgs &a, int b, int d, int c) {
     long long len, xoff, ooff;
     if (a.qsl != nullptr) {
@@ -82,7 +97,8 @@ __device__ __forceinline__ void conv1d_body(const ConvArgs &a, int b, int d, int
 
     float wv[W];
 #pragma unroll
-    for (int k = 0; k < W; ++k) wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
+    for (int k = 0; k < W; ++k)
+        wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
     const float bv = a.bias ? h2f(a.bias[d]) : 0.0f;
 
     // win[k] = full_x value at sequence position t0 - (W-1) + k
@@ -120,7 +136,7 @@ __device__ __forceinline__ void conv1d_body(const ConvArgs &a, int b, int d, int
         float acc = 0.0f;
 #pragma unroll
         for (int k = 0; k < W; ++k) acc += win[j + k] * wv[k];
-        o[j] = act(acc + bv, a.silu);
+        o[j] = act<SILU>(acc + bv);
     }
     if (SEQ_CONTIG && full && tecoops::aligned(outr + t0, 16)) {
 #pragma unroll
@@ -128,7 +144,7 @@ __device__ __forceinline__ void conv1d_body(const ConvArgs &a, int b, int d, int
             uint4 q;
             uint32_t *pq = reinterpret_cast<uint32_t *>(&q);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) pq[j] = pack<f16>(o[8 * v + 2 * j], o[8 * v + 2 * j + 1]);
+            for (int j = 0; j < 4; ++j) pq[j] = pack_h2(o[8 * v + 2 * j], o[8 * v + 2 * j + 1]);
             *reinterpret_cast<uint4 *>(outr + t0 + 8 * v) = q;
         }
     } else {
@@ -165,7 +181,7 @@ __device__ __forceinline__ void conv1d_body(const ConvArgs &a, int b, int d, int
 constexpr int kSegs = 4;
 constexpr int kRowsPerWave = 1;
 
-template <int W>
+template <int W, bool SILU>
 __global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {
     constexpr int CH = 8, SEG = 64 * CH;
     const int lane = threadIdx.x & 63;
@@ -197,7 +213,8 @@ __global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {
         const bool vec_row = tecoops::aligned(xr, 16) && tecoops::aligned(outr, 16);
         float wv[W];
 #pragma unroll
-        for (int k = 0; k < W; ++k) wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
+        for (int k = 0; k < W; ++k)
+            wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
         const float bv = a.bias ? h2f(a.bias[d]) : 0.0f;
         // prefix[k]: full_x at position k - (W-1), the old state or zeros
         uint16_t prefix[W - 1];
@@ -259,14 +276,14 @@ __global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {
                     float acc = 0.0f;
 #pragma unroll
                     for (int k = 0; k < W; ++k) acc += win[j + k] * wv[k];
-                    o[j] = act(acc + bv, a.silu);
+                    o[j] = act<SILU>(acc + bv);
                 }
                 if (vec_row && t0 + CH <= len) {
                     uint4 q;
-                    q.x = pack<f16>(o[0], o[1]);
-                    q.y = pack<f16>(o[2], o[3]);
-                    q.z = pack<f16>(o[4], o[5]);
-                    q.w = pack<f16>(o[6], o[7]);
+                    q.x = pack_h2(o[0], o[1]);
+                    q.y = pack_h2(o[2], o[3]);
+                    q.z = pack_h2(o[4], o[5]);
+                    q.w = pack_h2(o[6], o[7]);
                     st_stream(reinterpret_cast<uint4 *>(outr + t0), q);
                 } else {
 #pragma unroll
@@ -297,7 +314,240 @@ __global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {
     }
 }
 
-template <int W, bool SEQ_CONTIG, int CH>
+// ------------------------------------------------ channel-contiguous tokens
+
+constexpr int kTokChunk = 8;    // tokens per lane (4 measured alike, 16 slower)
+constexpr int kTokSlab = 512;   // channels per wave (64 lanes x 8)
+
+// A sequence of the global token axis: index b, tokens [s, e); b < 0 when the
+// token lies in no sequence.
+struct SeqSpan {
+    int b;
+    long long s, e;
+};
+
+// The sequence holding global token t.  With query_start_loc, the largest b
+// with qsl[b] <= t (empty sequences before it share its start); otherwise
+// sequence t / seq_len.
+__device__ __forceinline__ SeqSpan seq_of(const ConvArgs &a, long long t) {
+    SeqSpan r{-1, 0, 0};
+    if (a.qsl == nullptr) {
+        const long long b = t / a.seq_len;
+        if (t < 0 || b >= a.batch) return r;
+        r.b = static_cast<int>(b);
+        r.s = b * a.seq_len;
+        r.e = r.s + a.seq_len;
+        return r;
+    }
+    if (t < a.qsl[0] || t >= a.qsl[a.batch]) return r;
+    int lo = 0, hi = a.batch - 1;  // qsl[lo] <= t
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.qsl[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    r.b = lo;
+    r.s = a.qsl[lo];
+    r.e = a.qsl[lo + 1];
+    return r;
+}
+
+// Element offsets of token t of sequence sp in x and out.
+__device__ __forceinline__ long long x_off(const ConvArgs &a, const SeqSpan &sp, long long t) {
+    return a.qsl ? t * a.xs : sp.b * a.xb + (t - sp.s) * a.xs;
+}
+__device__ __forceinline__ long long o_off(const ConvArgs &a, const SeqSpan &sp, long long t) {
+    return a.qsl ? t * a.os : sp.b * a.ob + (t - sp.s) * a.os;
+}
+
+__device__ __forceinline__ void unpack8(const uint4 &q, float (&v)[8]) {
+    v[0] = lo<f16>(q.x); v[1] = hi<f16>(q.x); v[2] = lo<f16>(q.y); v[3] = hi<f16>(q.y);
+    v[4] = lo<f16>(q.z); v[5] = hi<f16>(q.z); v[6] = lo<f16>(q.w); v[7] = hi<f16>(q.w);
+}
+
+// Conv state row r (0 .. W-2: full_x position r - (W-1)) of the 8 channels at
+// d0 for cache entry cidx.
+__device__ __forceinline__ uint4 *state_row(const ConvArgs &a, int cidx, int r, int d0) {
+    return reinterpret_cast<uint4 *>(a.state + static_cast<long long>(cidx) * a.state_stride +
+                                     static_cast<long long>(r) * a.dim + d0);
+}
+
+// Output row of token t (sequence sp) for the 8 channels at d0, its window
+// read from x and, for positions before the sequence start, from the old
+// state (or zeros).  The boundary path of conv1d_tokens_kernel.
+template <int W, bool SILU>
+__device__ __forceinline__ void token_row(const ConvArgs &a, const SeqSpan &sp, int cidx,
+                                          bool use_state, long long t, int d0,
+                                          const float (&wv)[W][8], const float (&bv)[8]) {
+    float acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = bv[c];
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+        const long long pos = t - (W - 1) + k;
+        uint4 q = {0u, 0u, 0u, 0u};
+        if (pos >= sp.s)
+            q = *reinterpret_cast<const uint4 *>(a.x + x_off(a, sp, pos) + d0);
+        else if (use_state)
+            q = *state_row(a, cidx, static_cast<int>(pos - sp.s + (W - 1)), d0);
+        float v[8];
+        unpack8(q, v);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] += v[c] * wv[k][c];
+    }
+    uint4 o;
+    o.x = pack_h2(act<SILU>(acc[0]), act<SILU>(acc[1]));
+    o.y = pack_h2(act<SILU>(acc[2]), act<SILU>(acc[3]));
+    o.z = pack_h2(act<SILU>(acc[4]), act<SILU>(acc[5]));
+    o.w = pack_h2(act<SILU>(acc[6]), act<SILU>(acc[7]));
+    *reinterpret_cast<uint4 *>(a.out + o_off(a, sp, t) + d0) = o;
+}
+
+// Channel-contiguous layout ([tokens, dim] rows, dim % 8 == 0, 16-byte
+// aligned rows): work item (chunk, slab) covers tokens [8 chunk, +8) of the
+// global token axis and channels [2048 slab, +2048), wave w and lane l
+// channels [2048 slab + 512 w + 8 l, +8) as one 16-byte vector per token.
+// Work items are dealt to the 8 XCDs in contiguous ranges (workgroup n runs
+// on XCD n % 8), so the W-1 rows before a chunk, which the previous chunk
+// loaded, are L2 hits.
+//
+// A chunk inside one sequence and at least W-1 tokens past its start loads
+// its W-1 + 8 rows at once and convolves them in registers.  Rows that no
+// other chunk reads go through the non-temporal path; the window (the W-1
+// rows before the chunk, read last here) and the chunk's last W-1 rows (the
+// next chunk's window) stay in L2.  Measured at the BASELINE shape: 48.9 us,
+// against 55.6 us with every load plain, 57.6 us with every load
+// non-temporal (the next chunk's window then misses L2) and 52.8 us with
+// the window non-temporal too; passing the window between the waves of a
+// workgroup through LDS instead of L2 cost a barrier and ran 49.5 us.
+//
+// Other chunks take their tokens one at a time (token_row), by this
+// ownership rule: a token within W-1 of its sequence's start belongs to the
+// chunk holding that start (even past the chunk's end), every other token to
+// the chunk holding it.  Only the chunk holding a sequence's start then reads
+// the sequence's old conv state, and it writes the new state after its
+// tokens, so no lane reads a state another lane writes.
+template <int W, bool SILU>
+__global__ void __launch_bounds__(256) conv1d_tokens_kernel(ConvArgs a, long long nitems,
+                                                            long long per_xcd, int nslabs) {
+    constexpr int CH = kTokChunk;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const long long item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (item >= nitems) return;
+    const long long t0 = (item / nslabs) * CH;
+    const int d0 = static_cast<int>(item % nslabs) * (4 * kTokSlab) + wave * kTokSlab + lane * 8;
+    if (d0 >= a.dim) return;
+    const SeqSpan sp = seq_of(a, t0);
+    if (sp.b < 0 && t0 >= (a.qsl ? a.qsl[a.batch] : static_cast<long long>(a.batch) * a.seq_len))
+        return;  // past the last sequence
+
+    float wv[W][8], bv[8];
+    if (a.wd == 1 && a.ww % 8 == 0 && tecoops::aligned(a.w, 16)) {
+        // channel-contiguous weight ([width, dim], the reference layout)
+#pragma unroll
+        for (int k = 0; k < W; ++k)
+            unpack8(*reinterpret_cast<const uint4 *>(a.w + static_cast<long long>(k) * a.ww + d0),
+                    wv[k]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < W; ++k)
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                wv[k][c] = h2f(a.w[static_cast<long long>(d0 + c) * a.wd + k * a.ww]);
+    }
+    if (a.bias != nullptr && tecoops::aligned(a.bias, 16)) {
+        unpack8(*reinterpret_cast<const uint4 *>(a.bias + d0), bv);
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) bv[c] = a.bias ? h2f(a.bias[d0 + c]) : 0.0f;
+    }
+
+    const int cidx0 = sp.b >= 0 ? (a.cidx ? a.cidx[sp.b] : sp.b) : 0;
+    if (sp.b >= 0 && t0 - sp.s >= W - 1 && t0 + CH <= sp.e) {
+        if (cidx0 == a.pad_slot_id) return;
+        // rows t0 - (W-1) .. t0 + CH - 1, all inside the sequence
+        const uint16_t *xr = a.x + x_off(a, sp, t0 - (W - 1)) + d0;
+        uint4 raw[W - 1 + CH];
+#pragma unroll
+        for (int j = 0; j < W - 1 + CH; ++j) {
+            const uint4 *p = reinterpret_cast<const uint4 *>(xr + j * a.xs);
+            raw[j] = (j >= W - 1 && j < CH) ? ld_stream(p) : *p;
+        }
+        float win[W][8];
+#pragma unroll
+        for (int k = 0; k < W - 1; ++k) unpack8(raw[k], win[k + 1]);
+        uint16_t *outr = a.out + o_off(a, sp, t0) + d0;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+#pragma unroll
+            for (int k = 0; k < W - 1; ++k)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) win[k][c] = win[k + 1][c];
+            unpack8(raw[W - 1 + j], win[W - 1]);
+            float o[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                float acc = bv[c];
+#pragma unroll
+                for (int k = 0; k < W; ++k) acc += win[k][c] * wv[k][c];
+                o[c] = act<SILU>(acc);
+            }
+            uint4 q;
+            q.x = pack_h2(o[0], o[1]);
+            q.y = pack_h2(o[2], o[3]);
+            q.z = pack_h2(o[4], o[5]);
+            q.w = pack_h2(o[6], o[7]);
+            st_stream(reinterpret_cast<uint4 *>(outr + j * a.os), q);
+        }
+        return;
+    }
+
+    // Boundary chunk: its tokens one at a time, by the ownership rule.
+    SeqSpan cur = sp;
+    for (long long t = t0; t < t0 + CH + W - 2; ++t) {
+        if (cur.b < 0 || t >= cur.e) cur = seq_of(a, t);
+        if (cur.b < 0) continue;
+        const bool owned = t - cur.s >= W - 1 ? t < t0 + CH : (cur.s >= t0 && cur.s < t0 + CH);
+        if (!owned) continue;
+        const int cidx = a.cidx ? a.cidx[cur.b] : cur.b;
+        if (cidx == a.pad_slot_id) continue;
+        const bool use_state = a.state != nullptr &&
+                               (a.api_mode == 1 || (a.hinit != nullptr && a.hinit[cur.b] != 0));
+        token_row<W, SILU>(a, cur, cidx, use_state, t, d0, wv, bv);
+    }
+    // New conv states of the (non-empty) sequences that start in this chunk:
+    // the last W-1 entries of full_x, read (x, or the old state for short
+    // sequences) before any is written.
+    if (a.state == nullptr) return;
+    int b = sp.b >= 0 ? sp.b : 0;
+    if (sp.b >= 0 && sp.s < t0) ++b;
+    for (; b < a.batch; ++b) {
+        SeqSpan q;
+        q.b = b;
+        q.s = a.qsl ? a.qsl[b] : static_cast<long long>(b) * a.seq_len;
+        q.e = a.qsl ? a.qsl[b + 1] : q.s + a.seq_len;
+        if (q.s >= t0 + CH) break;
+        if (q.s < t0 || q.e <= q.s) continue;
+        const int cidx = a.cidx ? a.cidx[b] : b;
+        if (cidx == a.pad_slot_id) continue;
+        const bool use_state = a.api_mode == 1 || (a.hinit != nullptr && a.hinit[b] != 0);
+        uint4 ns[W - 1];
+#pragma unroll
+        for (int k = 0; k < W - 1; ++k) {
+            const long long pos = q.e - (W - 1) + k;
+            uint4 v = {0u, 0u, 0u, 0u};
+            if (pos >= q.s)
+                v = *reinterpret_cast<const uint4 *>(a.x + x_off(a, q, pos) + d0);
+            else if (use_state)
+                v = *state_row(a, cidx, static_cast<int>(pos - q.s + (W - 1)), d0);
+            ns[k] = v;
+        }
+#pragma unroll
+        for (int k = 0; k < W - 1; ++k) *state_row(a, cidx, k, d0) = ns[k];
+    }
+}
+
+template <int W, bool SEQ_CONTIG, int CH, bool SILU>
 __global__ void __launch_bounds__(256) conv1d_kernel(ConvArgs a) {
     // SEQ_CONTIG: grid (chunk blocks, channels, batch), chunk fastest;
     // otherwise: grid (channel blocks, chunks, batch), channel fastest.
@@ -307,23 +557,46 @@ __global__ void __launch_bounds__(256) conv1d_kernel(ConvArgs a) {
         const int c = SEQ_CONTIG ? lin : y;
         const int d = SEQ_CONTIG ? y : lin;
         if ((SEQ_CONTIG ? c >= a.nchunks : d >= a.dim)) return;
-        conv1d_body<W, SEQ_CONTIG, CH>(a, b, d, c);
+        conv1d_body<W, SEQ_CONTIG, CH, SILU>(a, b, d, c);
     }
 }
 
-template <int W>
+// The channel-contiguous kernel's preconditions: channel stride 1 in x and
+// out, 8-channel vectors 16-byte aligned everywhere they are read or written.
+bool tokens_layout(const ConvArgs &a) {
+    using tecoops::aligned;
+    if (a.xd != 1 || a.od != 1 || a.dim % 8 != 0) return false;
+    if (!aligned(a.x, 16) || !aligned(a.out, 16) || a.xs % 8 || a.os % 8) return false;
+    if (a.qsl == nullptr && (a.xb % 8 || a.ob % 8)) return false;
+    if (a.state != nullptr && (!aligned(a.state, 16) || a.state_stride % 8)) return false;
+    return true;
+}
+
+template <int W, bool SILU>
 void launch(const ConvArgs &a0, bool seq_contig, long long max_len, hipStream_t s) {
     ConvArgs a = a0;
+    if (!seq_contig && tokens_layout(a)) {
+        // global token axis: sum of lengths bounded by max_len with
+        // query_start_loc, batch * seq_len without
+        const long long tokens = a.qsl ? max_len : static_cast<long long>(a.batch) * a.seq_len;
+        const long long chunks = (tokens + kTokChunk - 1) / kTokChunk;
+        const int nslabs = static_cast<int>(tecoops::ceil_div(a.dim, 4 * kTokSlab));
+        const long long nitems = chunks * nslabs;
+        const long long per_xcd = (nitems + 7) / 8;
+        hipLaunchKernelGGL((conv1d_tokens_kernel<W, SILU>), dim3(static_cast<unsigned>(8 * per_xcd)),
+                           dim3(256), 0, s, a, nitems, per_xcd, nslabs);
+        return;
+    }
     if (seq_contig) {
         (void)max_len;
         const long long rows = static_cast<long long>(a.batch) * a.dim;
         const unsigned grid = static_cast<unsigned>(tecoops::ceil_div(rows, 4LL * kRowsPerWave));
-        hipLaunchKernelGGL((conv1d_rows_kernel<W>), dim3(grid), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((conv1d_rows_kernel<W, SILU>), dim3(grid), dim3(256), 0, s, a);
     } else {
         constexpr int CH = 16;
         a.nchunks = static_cast<int>((max_len + CH - 1) / CH);
         dim3 grid(tecoops::ceil_div(a.dim, 256), a.nchunks < 65535 ? a.nchunks : 65535, a.batch);
-        hipLaunchKernelGGL((conv1d_kernel<W, false, CH>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((conv1d_kernel<W, false, CH, SILU>), grid, dim3(256), 0, s, a);
     }
 }
 
@@ -366,10 +639,14 @@ extern "C" tecoopsStatus_t tecoopsCausalConv1dEx(
     a.api_mode = api_mode;
     a.silu = silu != 0;
     const bool seq_contig = xSeqStride == 1 && outSeqStride == 1;
-    switch (width) {
-        case 2: launch<2>(a, seq_contig, seqLen, handle->stream); break;
-        case 3: launch<3>(a, seq_contig, seqLen, handle->stream); break;
-        default: launch<4>(a, seq_contig, seqLen, handle->stream); break;
+    hipStream_t st = handle->stream;
+    switch (width * 2 + (a.silu ? 1 : 0)) {
+        case 4: launch<2, false>(a, seq_contig, seqLen, st); break;
+        case 5: launch<2, true>(a, seq_contig, seqLen, st); break;
+        case 6: launch<3, false>(a, seq_contig, seqLen, st); break;
+        case 7: launch<3, true>(a, seq_contig, seqLen, st); break;
+        case 8: launch<4, false>(a, seq_contig, seqLen, st); break;
+        default: launch<4, true>(a, seq_contig, seqLen, st); break;
     }
     TECO_CHECK_LAUNCH("causal_conv1d");
     return TECOOPS_STATUS_SUCCESS;

@@ -398,6 +398,101 @@ def test_causal_conv1d_reference_layout_long_varlen():
     assert np.array_equal(host_bits(st_dev), st_ref)
 
 
+def _conv_c_api(x, w, st, qsl, cidx, hinit, pad, api_mode, W):
+    """tecoopsCausalConv1d on token-major x [tokens, dim] (the reference C
+    layout); returns out and the updated state as numpy bits."""
+    import ctypes
+    from tecoops import _lib
+    total, dim = x.shape
+    xd, wd, sd, qd = dev(x), dev(w), dev(st), dev(qsl)
+    cd = dev(cidx) if cidx is not None else None
+    hd = dev(hinit) if hinit is not None else None
+    out = torch.full((total, dim), float("nan"), dtype=torch.float16, device="cuda")
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    _lib.call("tecoopsCausalConv1d", tecoops._handle(xd.device), len(qsl) - 1, total, dim, W,
+              (W - 1) * dim, dim, dim, pad, api_mode, 0, p(xd), p(sd), p(wd), p(out), p(qd),
+              p(cd), p(hd))
+    torch.cuda.synchronize()
+    return host_bits(out), host_bits(sd)
+
+
+def test_causal_conv1d_token_major_baseline_shape():
+    """The BASELINE conv shape in the reference C layout: x [8 x 2048 tokens,
+    4096] token-major through tecoopsCausalConv1d, weight [4, 4096], no
+    initial state, final state written (16-byte channel vectors)."""
+    r = rng(78)
+    dim, lens = 4096, [2048] * 8
+    total = sum(lens)
+    x = bits(r.standard_normal((total, dim), dtype=np.float32))
+    w = bits(r.normal(0, 0.5, (4, dim)).astype(np.float32))
+    st = bits(r.standard_normal((8, 3, dim), dtype=np.float32))
+    qsl = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    hinit = np.zeros(8, np.int8)
+    st_ref = st.copy()
+    ref = orc.causal_conv1d(x, w, conv_state=st_ref, query_start_loc=qsl,
+                            has_initial_state=hinit, layout="ld")
+    out, st_got = _conv_c_api(x, w, st, qsl, None, hinit, -1, 0, 4)
+    assert_close(orc.to_float(out), ref, what="conv token-major 16384x4096")
+    assert np.array_equal(st_got, st_ref)
+
+
+@pytest.mark.parametrize("W", [4, 3, 2])
+@pytest.mark.parametrize("dim", [2056, 104, 100])
+def test_causal_conv1d_token_major_boundaries(W, dim):
+    """Token-major sequences whose starts fall on every position of a 16-token
+    chunk (among them the last two, whose first tokens belong to the chunk
+    before), empty and one-token sequences, a padded slot, mixed initial
+    states, api_mode 0; dim 2056 spans a partial 2048-channel slab and 100 is
+    not a multiple of 8 (the 2-byte path)."""
+    r = rng(300 + W + dim)
+    lens = [14, 1, 0, 17, 15, 2, 33, 16, 1, 0, 47, 3]
+    total = sum(lens)
+    n = len(lens)
+    x = bits(r.standard_normal((total, dim), dtype=np.float32))
+    w = bits(r.normal(0, 0.5, (W, dim)).astype(np.float32))
+    st = bits(r.standard_normal((n + 1, W - 1, dim), dtype=np.float32))
+    qsl = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cidx = np.array([3, 0, 1, 2, 12, 5, 4, 7, 6, 9, 8, 11], np.int32)
+    cidx[5] = 99        # padded slot: skipped
+    hinit = (r.integers(0, 2, n)).astype(np.int8)
+    st_ref = st.copy()
+    ref = orc.causal_conv1d(x, w, conv_state=st_ref, query_start_loc=qsl, cache_indices=cidx,
+                            has_initial_state=hinit, pad_slot_id=99, layout="ld")
+    out, st_got = _conv_c_api(x, w, st, qsl, cidx, hinit, 99, 0, W)
+    got = orc.to_float(out)
+    pad_rows = slice(qsl[5], qsl[6])
+    assert np.isnan(got[pad_rows]).all(), "padded sequence was written"
+    keep = np.ones(total, bool)
+    keep[pad_rows] = False
+    assert_close(got[keep], ref[keep], what=f"conv token-major W={W} dim={dim}")
+    assert np.array_equal(st_got, st_ref)
+
+
+def test_causal_conv1d_token_major_ex_batch_strides():
+    """tecoopsCausalConv1dEx on [B, L, D] storage (no query_start_loc: batch
+    strides) with bias and state, through tecoops.causal_conv1d on a
+    [B, D, L] view."""
+    r = rng(310)
+    B, L, dim = 3, 530, 1032
+    xs = bits(r.standard_normal((B, L, dim), dtype=np.float32))
+    w = bits(r.normal(0, 0.5, (dim, 4)).astype(np.float32))
+    bias = bits(r.standard_normal(dim, dtype=np.float32))
+    st = bits(r.standard_normal((B, 3, dim), dtype=np.float32))
+    hinit = np.array([1, 0, 1], np.int8)
+    st_ref = st.copy()
+    x_bdl = np.ascontiguousarray(xs.transpose(0, 2, 1))
+    ref = orc.causal_conv1d(x_bdl, w, bias=bias, conv_state=st_ref, has_initial_state=hinit,
+                            layout="bdl")
+    xt = dev(xs).permute(0, 2, 1)
+    out = torch.empty((B, L, dim), dtype=torch.float16, device="cuda").permute(0, 2, 1)
+    st_dev = dev(st)
+    tecoops.causal_conv1d(xt, dev(w), dev(bias), out, conv_states=st_dev,
+                          has_initial_state=dev(hinit))
+    torch.cuda.synchronize()
+    assert_close(as_f32(out.permute(0, 2, 1)).transpose(0, 2, 1), ref, what="conv [B, L, D]")
+    assert np.array_equal(host_bits(st_dev), st_ref)
+
+
 def test_causal_conv1d_baseline_config():
     """BASELINE config: x fp16 [8, 4096, 2048] ~N(0,1), weight [4096, 4]
     ~N(0,0.5), bias [4096] ~N(0,1), SiLU, final state written."""
