@@ -281,8 +281,12 @@ struct PagedLoader128 {
     static __device__ __forceinline__ int group_page(const FaParams &p, const int *bt_row,
                                                      int row0, int kv_limit) {
         row0 = __builtin_amdgcn_readfirstlane(row0);
-        const int page = row0 < kv_limit ? bt_row[row0 >> p.lbs] : 0;
-        return __builtin_amdgcn_readfirstlane(page);
+        // The block table is read-only for the launch: read through the
+        // constant address space, the wave-uniform entry is always a scalar
+        // load, so waiting for it never waits for the K/V vector loads in
+        // flight (a vector load here would, under s_waitcnt vmcnt).
+        const auto *bt4 = (const __attribute__((address_space(4))) int *)(bt_row);
+        return row0 < kv_limit ? bt4[row0 >> p.lbs] : 0;
     }
 
     // Element offset of the group's first row (page 0 when its id is out of range).
