@@ -785,17 +785,187 @@ __device__ __forceinline__ void merge_waves(const uint16_t *smem, int ncols, Sin
 // per pass over all its keys, which writes its output rows itself; the
 // combine kernel leaves it alone.  So the output never depends on the host's
 // bounds, only the speed does.
+// q length of sequence b.
+__device__ __forceinline__ int q_len_of(const FaParams &p, int b) {
+    return p.q_lens != nullptr ? p.q_lens[b] : p.cu_q[b + 1] - p.cu_q[b];
+}
+
+// Split-KV work items of a sequence with q length L and kv length S: every
+// split but the last is split_len keys long; the last holds the rest (up to
+// the end of the sequence).  A sequence whose q length exceeds the decode
+// bound rq, or that has no keys, is one item.
+__device__ __forceinline__ int decode_items(const FaParams &p, int L, int S) {
+    if (L <= 0 || L > p.rq || S <= 0) return 1;
+    return min((S + p.split_len - 1) / p.split_len, p.max_splits);
+}
+
+// Keys of the last item, scaled by its query passes (q lengths past rq take
+// several) and capped at INT_MAX; -1 for a sequence with no queries (nothing
+// to do).
+__device__ __forceinline__ int decode_last_work(const FaParams &p, int L, int S) {
+    if (L <= 0) return -1;
+    if (L > p.rq) {
+        const long long w = static_cast<long long>(S) * ((L + 32 / p.G - 1) / (32 / p.G));
+        return static_cast<int>(min(w, 0x7fffffffLL));
+    }
+    return S - (decode_items(p, L, S) - 1) * p.split_len;
+}
+
+// Workgroup i's work item in longest-first order: first the full split_len
+// items of every sequence (all the same size), then each (sequence, kv head)
+// last item, longest first (ties by sequence).  Without the ordering the
+// full splits of long sequences are dispatched last and run in the tail
+// (equal lengths with the same total keys took 183 us against 201 us for
+// lengths spread over 512..8192).  Wave 0 reads each sequence's lengths once
+// (lane t: sequences t, t + 64, ...), keeps what it derives in registers for
+// batches of up to 64, and leaves the choice in LDS; returns false for
+// workgroups past the last item.
+__device__ bool decode_item(const FaParams &p, int i, int &b, int &kvh, int &split,
+                            long long &q_off, int &L, int &S) {
+    __shared__ long long pick_off;
+    __shared__ int pick[4];  // sequence, item code, q length, kv length
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x < 64) {
+        if (lane == 0) pick[0] = -1;
+        int base = 0;        // full items of the sequences before this chunk
+        long long qb = 0;    // q rows of the sequences before this chunk
+        int w0 = -2;         // last-item work of sequence `lane` (first chunk)
+        int L0 = 0, S0 = 0;  // lengths of sequence `lane` (first chunk)
+        long long o0 = 0;    // q offset of sequence `lane` (first chunk)
+        for (int c0 = 0; c0 < p.batch; c0 += 64) {
+            const int t = c0 + lane;
+            int f = 0, w = -2, Lt = 0, St = 0;
+            long long ot = 0;
+            if (t < p.batch) {
+                Lt = q_len_of(p, t);
+                St = kv_len(p, t);
+                if (p.q_lens == nullptr) ot = p.cu_q[t];
+                f = (decode_items(p, Lt, St) - 1) * p.Hkv;
+                w = decode_last_work(p, Lt, St);
+            }
+            int x = f;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int v = __shfl_up(x, d, 64);
+                if (lane >= d) x += v;
+            }
+            long long xq = 0;
+            if (p.q_lens != nullptr) {  // q offsets: exclusive prefix of the q lengths
+                xq = t < p.batch ? Lt : 0;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const long long vq = __shfl_up(xq, d, 64);
+                    if (lane >= d) xq += vq;
+                }
+                ot = qb + xq - Lt;
+            }
+            if (c0 == 0) {
+                w0 = w;
+                L0 = Lt;
+                S0 = St;
+                o0 = ot;
+            }
+            const int pre = base + x - f;
+            if (t < p.batch && i >= pre && i < pre + f) {
+                pick[0] = t;
+                pick[1] = i - pre;
+                pick[2] = Lt;
+                pick[3] = St;
+                pick_off = ot;
+            }
+            base += __shfl(x, 63, 64);
+            qb += __shfl(xq, 63, 64);
+        }
+        const int j = i - base;
+        if (j >= 0 && j < p.batch * p.Hkv) {
+            // last items, longest first: the rank of lane t's sequence among
+            // 64 sequences at a time, broadcast from the lanes holding them
+            // (lanes past the batch hold -2 and rank below every sequence)
+            const int rank = j / p.Hkv;
+            long long qc = 0;  // q rows before chunk c0 (q_lens only)
+            for (int c0 = 0; c0 < p.batch; c0 += 64) {
+                const int t = c0 + lane;
+                int w = w0, Lt = L0, St = S0;
+                long long ot = o0;
+                if (c0 > 0) {
+                    w = -2;
+                    Lt = 0;
+                    St = 0;
+                    if (t < p.batch) {
+                        Lt = q_len_of(p, t);
+                        St = kv_len(p, t);
+                        w = decode_last_work(p, Lt, St);
+                    }
+                    long long xq = p.q_lens != nullptr ? Lt : 0;
+#pragma unroll
+                    for (int d = 1; d < 64; d <<= 1) {
+                        const long long vq = __shfl_up(xq, d, 64);
+                        if (lane >= d) xq += vq;
+                    }
+                    ot = p.q_lens != nullptr ? qc + xq - Lt : (t < p.batch ? p.cu_q[t] : 0);
+                    qc += __shfl(xq, 63, 64);
+                } else if (p.q_lens != nullptr) {
+                    long long xq = Lt;
+#pragma unroll
+                    for (int d = 1; d < 64; d <<= 1) {
+                        const long long vq = __shfl_up(xq, d, 64);
+                        if (lane >= d) xq += vq;
+                    }
+                    qc = __shfl(xq, 63, 64);
+                }
+                int r = 0;
+                // a batch whose last items are all the same size keeps
+                // sequence order, with no ranking
+                const bool same =
+                    p.batch <= 64 && __all(t >= p.batch || w == __builtin_amdgcn_readfirstlane(w));
+                if (same) r = t;
+                for (int u0 = 0; !same && u0 < p.batch; u0 += 64) {
+                    int wl = w0;
+                    if (u0 > 0)
+                        wl = u0 + lane < p.batch
+                                 ? decode_last_work(p, q_len_of(p, u0 + lane), kv_len(p, u0 + lane))
+                                 : -2;
+#pragma unroll
+                    for (int v = 0; v < 64; ++v) {
+                        // a scalar broadcast (v_readlane), not an LDS permute
+                        const int wu = __builtin_amdgcn_readlane(wl, v);
+                        r += (wu > w || (wu == w && u0 + v < t)) ? 1 : 0;
+                    }
+                }
+                if (t < p.batch && r == rank) {
+                    pick[0] = t;
+                    pick[1] = -1 - (j % p.Hkv);
+                    pick[2] = Lt;
+                    pick[3] = St;
+                    pick_off = ot;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    b = pick[0];
+    if (b < 0) return false;
+    const int r = pick[1];
+    L = pick[2];
+    S = pick[3];
+    q_off = pick_off;
+    if (r >= 0) {
+        kvh = r % p.Hkv;
+        split = r / p.Hkv;
+    } else {
+        kvh = -1 - r;
+        split = decode_items(p, L, S) - 1;
+    }
+    return true;
+}
+
 template <typename T, int D, bool POW2>
 __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) fa_decode_kernel(FaParams p) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    const int kvh = blockIdx.x % p.Hkv;
-    const int b = blockIdx.x / p.Hkv;
-    const int split = blockIdx.y;
+    int b, kvh, split, L, S;
     long long q_off;
-    int L;
-    seq_info(p, b, q_off, L);
+    if (!decode_item(p, blockIdx.y * gridDim.x + blockIdx.x, b, kvh, split, q_off, L, S)) return;
     if (L <= 0) return;
-    const int S = kv_len(p, b);
     if (L > p.rq) {
         if (split != 0) return;
         const int rq = 32 / p.G;
@@ -812,8 +982,7 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) fa_decode_kernel(FaParam
         return;
     }
     const int kv_lo = split * p.split_len;
-    if (split > 0 && kv_lo >= S) return;
-    const int kv_hi = split == static_cast<int>(gridDim.y) - 1 ? S : min(S, kv_lo + p.split_len);
+    const int kv_hi = split == decode_items(p, L, S) - 1 ? S : min(S, kv_lo + p.split_len);
     decode_pass<T, D, POW2>(p, smem, b, kvh, q_off, L, S, kv_lo, kv_hi, p.rq, 0);
     const long long base = ((static_cast<long long>(b) * p.Hkv + kvh) * p.max_splits + split) *
                            p.ncols;

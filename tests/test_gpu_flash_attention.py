@@ -305,6 +305,31 @@ def test_decode_rows_past_max_seqlen_q():
         assert_close(got, ref, what=f"speculative H={H}/{Hkv}")
 
 
+@pytest.mark.parametrize("entry", ["cu_seqlens", "q_seq_lens"])
+def test_decode_work_order_large_batch(entry):
+    """The decode kernel hands out its split-KV items longest first, from the
+    lengths of the whole batch, 64 sequences at a time.  150 sequences (three
+    chunks) with empty kv, single-split, multi-split and equal lengths, and
+    rows past max_seqlen_q = 1 (the whole-sequence item), through both q
+    length conventions; every row matches the oracle."""
+    r = np.random.default_rng(77)
+    kv = r.integers(1, 5000, 150)
+    kv[[3, 70, 149]] = 0
+    kv[10:20] = 2048
+    kv = kv.tolist()
+    q_lens = [1] * 150
+    for i in (5, 66, 130):
+        q_lens[i] = 3
+    q, kc, vc, bt = make_inputs(78, 8, 2, 128, 16, q_lens, [max(s, 1) for s in kv],
+                                dtype=orc.BF16, dist="normal")
+    if entry == "cu_seqlens":
+        got = run_gpu(q, kc, vc, bt, q_lens, kv, orc.BF16, max_q=1)
+    else:
+        got = run_reference_entry(q, kc, vc, bt, q_lens, kv, 1, 1, dtype=orc.BF16)
+    ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=orc.BF16)
+    assert_close(got, ref, what=f"decode order, 150 sequences ({entry})")
+
+
 def test_prefill_rows_past_max_seqlen_q():
     """Prefill grid sized from an understated max_seqlen_q: workgroups take the
     query tiles past the grid in turn."""
