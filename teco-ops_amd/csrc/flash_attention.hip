@@ -388,6 +388,15 @@ template <> struct Ones2<f16> {
     }
 };
 
+// Max of one lane's 16 scores as a tree of three-input maxima (v_max3_f32):
+// 8 instructions, 3 deep.
+__device__ __forceinline__ float max16(const f32x16_t &s) {
+    const auto m3 = [](float a, float b, float c) { return fmaxf(fmaxf(a, b), c); };
+    const float a0 = m3(s[0], s[1], s[2]), a1 = m3(s[3], s[4], s[5]), a2 = m3(s[6], s[7], s[8]);
+    const float a3 = m3(s[9], s[10], s[11]), a4 = m3(s[12], s[13], s[14]);
+    return fmaxf(m3(a0, a1, a2), m3(a3, a4, s[15]));
+}
+
 // One wave's online-softmax attention over NKB 32-key blocks staged in LDS at
 // rows [kv_row0, kv_row0 + 32*NKB).  Lane l owns query column (l % 32) of each
 // of its QSUB column blocks.
@@ -424,7 +433,6 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
 #pragma unroll
     for (int qs = 0; qs < QSUB; ++qs) {
         // masked scores, then their max as a tree (short dependency chain)
-        float t4[NKB * 4];
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -433,17 +441,9 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
                 if (MASK && !(32 * kb + 8 * (v >> 2) + (v & 3) < lim[qs])) x = kNegInf;
                 s[kb][qs][v] = x;
             }
+        float mx = max16(s[0][qs]);
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                t4[kb * 4 + u] = fmaxf(fmaxf(s[kb][qs][4 * u], s[kb][qs][4 * u + 1]),
-                                       fmaxf(s[kb][qs][4 * u + 2], s[kb][qs][4 * u + 3]));
-#pragma unroll
-        for (int w = NKB * 4; w > 1; w >>= 1)
-#pragma unroll
-            for (int u = 0; u < w / 2; ++u) t4[u] = fmaxf(t4[u], t4[u + w / 2]);
-        float mx = t4[0];
+        for (int kb = 1; kb < NKB; ++kb) mx = fmaxf(mx, max16(s[kb][qs]));
         mx = half_swap_max(mx) * scale_log2;
         if (!__all(mx <= m[qs] + kRescaleSlack)) {
             const float m_new = fmaxf(m[qs], mx);  // m >= 0 keeps the reference clamp
