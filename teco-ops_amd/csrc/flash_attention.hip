@@ -410,7 +410,7 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
                                             const u32x4 (&qf)[QSUB][D / 16],
                                             f32x16_t (&oacc)[QSUB][D / 32], float (&m)[QSUB],
                                             float (&lsum)[QSUB], const int (&lim)[QSUB],
-                                            float scale_log2) {
+                                            float scale_log2, bool mask = MASK) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 5, r32 = lane & 31;
     f32x16_t s[NKB][QSUB];
@@ -433,14 +433,16 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
 #pragma unroll
     for (int qs = 0; qs < QSUB; ++qs) {
         // masked scores, then their max as a tree (short dependency chain)
+        if (MASK && mask) {
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                float x = s[kb][qs][v];
-                if (MASK && !(32 * kb + 8 * (v >> 2) + (v & 3) < lim[qs])) x = kNegInf;
-                s[kb][qs][v] = x;
-            }
+                for (int v = 0; v < 16; ++v) {
+                    float x = s[kb][qs][v];
+                    if (!(32 * kb + 8 * (v >> 2) + (v & 3) < lim[qs])) x = kNegInf;
+                    s[kb][qs][v] = x;
+                }
+        }
         float mx = max16(s[0][qs]);
 #pragma unroll
         for (int kb = 1; kb < NKB; ++kb) mx = fmaxf(mx, max16(s[kb][qs]));
@@ -524,8 +526,9 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
     const int qw0 = q0 + (wave / HW) * WROWS;
     const int q_start = p.causal ? max(S - L, 0) : 0;
     const int kv_end = p.causal ? min(S, q_start + min(q0 + QT, L)) : S;
-    const int wave_kv_end = p.causal ? min(S, q_start + min(qw0 + WROWS, L)) : S;
-    const int wave_min_vis = p.causal ? min(S, q_start + qw0 + 1) : S;
+    const int wave_kv_end =
+        __builtin_amdgcn_readfirstlane(p.causal ? min(S, q_start + min(qw0 + WROWS, L)) : S);
+    const int wave_min_vis = __builtin_amdgcn_readfirstlane(p.causal ? min(S, q_start + qw0 + 1) : S);
     const int *bt_row = p.bt + b * p.bt_stride;
     const long long head_off = static_cast<long long>(kvh) * p.bs * D;
 
@@ -574,12 +577,10 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
                 int lim[QSUB];
 #pragma unroll
                 for (int qs = 0; qs < QSUB; ++qs) lim[qs] = vis[qs] - j0 - 4 * g;
-                if (j0 + KB > wave_min_vis)
-                    wave_attend<T, D, KP, VP, NKB, QSUB, true>(cur, cur + TILE * KP, KB * hb, qf,
-                                                               oacc, m, lsum, lim, p.scale_log2);
-                else
-                    wave_attend<T, D, KP, VP, NKB, QSUB, false>(cur, cur + TILE * KP, KB * hb, qf,
-                                                                oacc, m, lsum, lim, p.scale_log2);
+                // one copy of the block code; the mask is a uniform branch
+                wave_attend<T, D, KP, VP, NKB, QSUB, true>(cur, cur + TILE * KP, KB * hb, qf, oacc, m,
+                                                           lsum, lim, p.scale_log2,
+                                                           j0 + KB > wave_min_vis);
             }
         }
         if (it + 1 < ntiles) ld.store(lds + ((it + 1) & 1) * Loader::ELEMS);
