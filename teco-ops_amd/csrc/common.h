@@ -8,8 +8,9 @@
 // least recently used replaced first): work on one stream is ordered by the
 // stream, and calls on different streams never share a buffer, so no event or
 // wait is needed.  Each buffer grows on demand on the device current at the
-// op; hipFree synchronises the device first, so a buffer still read by
-// enqueued work is never freed under it.
+// op, and a slot taken over from another stream gets a new buffer; hipFree
+// synchronises the device first, so a buffer still read by enqueued work is
+// never freed or reused under it.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -202,6 +202,17 @@ tecoopsStatus_t handle_scratch(tecoopsHandle_t handle, size_t bytes, void **out)
             }
             if (sl.last_use < slot->last_use) slot = &sl;
         }
+        // A buffer taken over from another stream may still be read by work
+        // enqueued there: free it (hipFree waits for the device) and let the
+        // allocation below start afresh.
+        if (slot->ptr != nullptr) {
+            const hipError_t e = hipFree(slot->ptr);
+            *slot = ScratchSlot{};
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                return TECOOPS_STATUS_INTERNAL_ERROR;
+            }
+        }
         slot->stream = handle->stream;
     }
     if (slot->bytes < bytes) {

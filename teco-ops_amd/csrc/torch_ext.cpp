@@ -15,8 +15,10 @@
 // two transposing copies (torch_ext.cpp:186-205).
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
+#include <ATen/ATen.h>
 #include <ATen/Tensor.h>
 
+#include <algorithm>
 #include <unordered_map>
 
 #include "tecoops.h"
@@ -150,13 +152,37 @@ void flash_attn_varlen_func(const Tensor &q, const Tensor &k, const Tensor &v,
     need_cuda({&q, &k, &v, &cu_seqlens_q, &seqused_k, &block_table, &out});
     const tecoopsDataType_t dt = dtype_of(q);
     Desc bt(block_table, TECOOPS_DATA_INT32), qd(q, dt), kd(k, dt), vd(v, dt), od(out, dt);
-    check(tecoopsFlashAttentionEx(handle_for(q), static_cast<int>(max_seqlen_q),
-                                  static_cast<int>(max_seqlen_k), nullptr,
+    // The split-KV workspace comes from torch's allocator: stream-ordered like
+    // any tensor, and taken from the graph's pool under CUDA-graph capture,
+    // where the handle's own scratch (hipMalloc on a stream's first use) could
+    // not be allocated.  The launch hints are the ones the library derives
+    // without a workspace (mean q length; max_seqlen_k capped by the
+    // block-table width * block size), so the plan and results are unchanged.
+    int q_hint = static_cast<int>(max_seqlen_q), k_hint = static_cast<int>(max_seqlen_k);
+    Tensor ws;
+    if (q.dim() == 3 && k.dim() == 4 && block_table.dim() == 2 && block_table.size(0) > 0) {
+        const int64_t batch = block_table.size(0);
+        const int64_t cap = std::min<int64_t>(block_table.size(1) * k.size(2), 0x7fffffff);
+        if (q_hint <= 0) q_hint = static_cast<int>(std::max<int64_t>(1, (q.size(0) + batch - 1) / batch));
+        k_hint = static_cast<int>(max_seqlen_k > 0 ? std::min<int64_t>(max_seqlen_k, cap) : cap);
+        size_t bytes = 0;
+        if (k_hint > 0 &&
+            tecoopsGetFlashAttentionWorkspaceSize(static_cast<int>(batch), static_cast<int>(q.size(1)),
+                                                  static_cast<int>(q.size(2)), q_hint, k_hint,
+                                                  &bytes) == TECOOPS_STATUS_SUCCESS &&
+            bytes > 0)
+            ws = at::empty({static_cast<int64_t>(bytes)}, q.options().dtype(at::kByte));
+    }
+    if (!ws.defined()) {
+        q_hint = static_cast<int>(max_seqlen_q);
+        k_hint = static_cast<int>(max_seqlen_k);
+    }
+    check(tecoopsFlashAttentionEx(handle_for(q), q_hint, k_hint, nullptr,
                                   cu_seqlens_q.data_ptr<int>(), seqused_k.data_ptr<int>(), bt.d,
                                   block_table.data_ptr(), qd.d, q.data_ptr(), kd.d, k.data_ptr(),
                                   vd.d, v.data_ptr(), od.d, out.data_ptr(),
                                   softmax_scale > 0 ? static_cast<float>(softmax_scale) : -1.0f,
-                                  causal ? 1 : 0, nullptr),
+                                  causal ? 1 : 0, ws.defined() ? ws.data_ptr() : nullptr),
           "flash_attn_varlen_func");
 }
 

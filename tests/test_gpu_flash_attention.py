@@ -400,6 +400,33 @@ def test_decode_on_two_streams(front):
         assert_close(as_f32(args[-1], orc.BF16), ref, what=f"{front} stream {i}")
 
 
+def test_decode_on_more_streams_than_scratch_slots():
+    """Decode calls round-robin over 10 streams through one handle, which
+    keeps split-KV scratch for 8: each call past the eighth stream takes over
+    another stream's buffer while that stream's work may still be queued.
+    No synchronisation between the calls; every result matches the oracle."""
+    r = np.random.default_rng(43)
+    runs = []
+    for i in range(10):
+        kv = r.integers(1500, 6000, 16).tolist()
+        q, kc, vc, bt = make_inputs(70 + i, 32, 8, 128, 16, [1] * 16, kv, dtype=orc.BF16)
+        cu = torch.arange(0, 17, dtype=torch.int32, device="cuda")
+        args = (dev(q, orc.BF16), dev(kc, orc.BF16), dev(vc, orc.BF16), 1, cu, max(kv), None,
+                dev(np.array(kv, np.int32)), 1.0 / math.sqrt(128), True, None, dev(bt), False,
+                torch.empty(q.shape, dtype=torch.bfloat16, device="cuda"))
+        runs.append((q, kc, vc, bt, kv, args))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(10)]
+    for rep in range(2):
+        for (q, kc, vc, bt, kv, args), st in zip(runs, streams):
+            with torch.cuda.stream(st):
+                tecoops.flash_attn_varlen_func(*args)
+    torch.cuda.synchronize()
+    for i, (q, kc, vc, bt, kv, args) in enumerate(runs):
+        ref = orc.flash_attention(q, kc, vc, bt, [1] * 16, kv, dtype=orc.BF16)
+        assert_close(as_f32(args[-1], orc.BF16), ref, what=f"stream {i} of 10")
+
+
 def test_decode_from_two_threads():
     """Two Python threads, each on its own stream, decode different batches
     concurrently through tecoops.*: each thread has its own handle."""
