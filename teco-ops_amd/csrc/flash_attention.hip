@@ -111,13 +111,17 @@ struct FaParams {
 // its relative precision in 16 bit.
 constexpr float kRescaleSlack = 8.0f;
 
+// With q_lens the offset is the sum of the lengths before b, taken by the 64
+// lanes of the wave in parallel (called by every lane of every wave).
 __device__ __forceinline__ void seq_info(const FaParams &p, int b, long long &q_off, int &L) {
     if (p.q_lens == nullptr) {
         q_off = p.cu_q[b];
         L = p.cu_q[b + 1] - p.cu_q[b];
     } else {
         long long off = 0;
-        for (int i = 0; i < b; ++i) off += p.q_lens[i];
+        for (int i = threadIdx.x & 63; i < b; i += 64) off += p.q_lens[i];
+#pragma unroll
+        for (int d = 32; d > 0; d >>= 1) off += __shfl_xor(off, d, 64);
         q_off = off;
         L = p.q_lens[b];
     }
@@ -812,134 +816,75 @@ __device__ __forceinline__ int decode_last_work(const FaParams &p, int L, int S)
     return S - (decode_items(p, L, S) - 1) * p.split_len;
 }
 
-// Workgroup i's work item in longest-first order: first the full split_len
-// items of every sequence (all the same size), then each (sequence, kv head)
-// last item, longest first (ties by sequence).  Without the ordering the
-// full splits of long sequences are dispatched last and run in the tail
-// (equal lengths with the same total keys took 183 us against 201 us for
-// lengths spread over 512..8192).  Wave 0 reads each sequence's lengths once
-// (lane t: sequences t, t + 64, ...), keeps what it derives in registers for
-// batches of up to 64, and leaves the choice in LDS; returns false for
-// workgroups past the last item.
+// Workgroup i's work item in longest-first order, for batches of up to 64
+// sequences: first the full split_len items of every sequence (all the same
+// size), then each (sequence, kv head) last item, longest first (ties by
+// sequence).  Without the ordering the full splits of long sequences are
+// dispatched last and run in the tail (equal lengths with the same total keys
+// took 183 us against 201 us for lengths spread over 512..8192).  Lane t of
+// wave 0 reads sequence t's lengths and leaves the choice in LDS; returns
+// false for workgroups past the last item.
 __device__ bool decode_item(const FaParams &p, int i, int &b, int &kvh, int &split,
                             long long &q_off, int &L, int &S) {
     __shared__ long long pick_off;
     __shared__ int pick[4];  // sequence, item code, q length, kv length
-    const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64) {
-        if (lane == 0) pick[0] = -1;
-        int base = 0;        // full items of the sequences before this chunk
-        long long qb = 0;    // q rows of the sequences before this chunk
-        int w0 = -2;         // last-item work of sequence `lane` (first chunk)
-        int L0 = 0, S0 = 0;  // lengths of sequence `lane` (first chunk)
-        long long o0 = 0;    // q offset of sequence `lane` (first chunk)
-        for (int c0 = 0; c0 < p.batch; c0 += 64) {
-            const int t = c0 + lane;
-            int f = 0, w = -2, Lt = 0, St = 0;
-            long long ot = 0;
-            if (t < p.batch) {
-                Lt = q_len_of(p, t);
-                St = kv_len(p, t);
-                if (p.q_lens == nullptr) ot = p.cu_q[t];
-                f = (decode_items(p, Lt, St) - 1) * p.Hkv;
-                w = decode_last_work(p, Lt, St);
-            }
-            int x = f;
+        const int t = threadIdx.x;
+        if (t == 0) pick[0] = -1;
+        int f = 0, w = -2, Lt = 0, St = 0;  // lanes past the batch: w = -2
+        long long ot = 0;
+        if (t < p.batch) {
+            Lt = q_len_of(p, t);
+            St = kv_len(p, t);
+            if (p.q_lens == nullptr) ot = p.cu_q[t];
+            f = (decode_items(p, Lt, St) - 1) * p.Hkv;  // full items
+            w = decode_last_work(p, Lt, St);
+        }
+        int x = f;  // inclusive prefix of the full items
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int v = __shfl_up(x, d, 64);
+            if (t >= d) x += v;
+        }
+        if (p.q_lens != nullptr) {  // q offsets: exclusive prefix of the q lengths
+            long long xq = Lt;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
-                const int v = __shfl_up(x, d, 64);
-                if (lane >= d) x += v;
+                const long long vq = __shfl_up(xq, d, 64);
+                if (t >= d) xq += vq;
             }
-            long long xq = 0;
-            if (p.q_lens != nullptr) {  // q offsets: exclusive prefix of the q lengths
-                xq = t < p.batch ? Lt : 0;
+            ot = xq - Lt;
+        }
+        const int pre = x - f;
+        if (t < p.batch && i >= pre && i < pre + f) {
+            pick[0] = t;
+            pick[1] = i - pre;
+            pick[2] = Lt;
+            pick[3] = St;
+            pick_off = ot;
+        }
+        const int j = i - __shfl(x, 63, 64);
+        if (j >= 0 && j < p.batch * p.Hkv) {
+            // last items, longest first: the rank of sequence t, from scalar
+            // broadcasts (v_readlane) of every lane's work; a batch whose
+            // last items are all the same size keeps sequence order
+            const int rank = j / p.Hkv;
+            int r = 0;
+            if (__all(t >= p.batch || w == __builtin_amdgcn_readfirstlane(w))) {
+                r = t;
+            } else {
 #pragma unroll
-                for (int d = 1; d < 64; d <<= 1) {
-                    const long long vq = __shfl_up(xq, d, 64);
-                    if (lane >= d) xq += vq;
+                for (int v = 0; v < 64; ++v) {
+                    const int wu = __builtin_amdgcn_readlane(w, v);
+                    r += (wu > w || (wu == w && v < t)) ? 1 : 0;
                 }
-                ot = qb + xq - Lt;
             }
-            if (c0 == 0) {
-                w0 = w;
-                L0 = Lt;
-                S0 = St;
-                o0 = ot;
-            }
-            const int pre = base + x - f;
-            if (t < p.batch && i >= pre && i < pre + f) {
+            if (t < p.batch && r == rank) {
                 pick[0] = t;
-                pick[1] = i - pre;
+                pick[1] = -1 - (j % p.Hkv);
                 pick[2] = Lt;
                 pick[3] = St;
                 pick_off = ot;
-            }
-            base += __shfl(x, 63, 64);
-            qb += __shfl(xq, 63, 64);
-        }
-        const int j = i - base;
-        if (j >= 0 && j < p.batch * p.Hkv) {
-            // last items, longest first: the rank of lane t's sequence among
-            // 64 sequences at a time, broadcast from the lanes holding them
-            // (lanes past the batch hold -2 and rank below every sequence)
-            const int rank = j / p.Hkv;
-            long long qc = 0;  // q rows before chunk c0 (q_lens only)
-            for (int c0 = 0; c0 < p.batch; c0 += 64) {
-                const int t = c0 + lane;
-                int w = w0, Lt = L0, St = S0;
-                long long ot = o0;
-                if (c0 > 0) {
-                    w = -2;
-                    Lt = 0;
-                    St = 0;
-                    if (t < p.batch) {
-                        Lt = q_len_of(p, t);
-                        St = kv_len(p, t);
-                        w = decode_last_work(p, Lt, St);
-                    }
-                    long long xq = p.q_lens != nullptr ? Lt : 0;
-#pragma unroll
-                    for (int d = 1; d < 64; d <<= 1) {
-                        const long long vq = __shfl_up(xq, d, 64);
-                        if (lane >= d) xq += vq;
-                    }
-                    ot = p.q_lens != nullptr ? qc + xq - Lt : (t < p.batch ? p.cu_q[t] : 0);
-                    qc += __shfl(xq, 63, 64);
-                } else if (p.q_lens != nullptr) {
-                    long long xq = Lt;
-#pragma unroll
-                    for (int d = 1; d < 64; d <<= 1) {
-                        const long long vq = __shfl_up(xq, d, 64);
-                        if (lane >= d) xq += vq;
-                    }
-                    qc = __shfl(xq, 63, 64);
-                }
-                int r = 0;
-                // a batch whose last items are all the same size keeps
-                // sequence order, with no ranking
-                const bool same =
-                    p.batch <= 64 && __all(t >= p.batch || w == __builtin_amdgcn_readfirstlane(w));
-                if (same) r = t;
-                for (int u0 = 0; !same && u0 < p.batch; u0 += 64) {
-                    int wl = w0;
-                    if (u0 > 0)
-                        wl = u0 + lane < p.batch
-                                 ? decode_last_work(p, q_len_of(p, u0 + lane), kv_len(p, u0 + lane))
-                                 : -2;
-#pragma unroll
-                    for (int v = 0; v < 64; ++v) {
-                        // a scalar broadcast (v_readlane), not an LDS permute
-                        const int wu = __builtin_amdgcn_readlane(wl, v);
-                        r += (wu > w || (wu == w && u0 + v < t)) ? 1 : 0;
-                    }
-                }
-                if (t < p.batch && r == rank) {
-                    pick[0] = t;
-                    pick[1] = -1 - (j % p.Hkv);
-                    pick[2] = Lt;
-                    pick[3] = St;
-                    pick_off = ot;
-                }
             }
         }
     }
@@ -965,7 +910,20 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) fa_decode_kernel(FaParam
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     int b, kvh, split, L, S;
     long long q_off;
-    if (!decode_item(p, blockIdx.y * gridDim.x + blockIdx.x, b, kvh, split, q_off, L, S)) return;
+    if (p.batch <= 64) {
+        if (!decode_item(p, blockIdx.y * gridDim.x + blockIdx.x, b, kvh, split, q_off, L, S))
+            return;
+    } else {
+        // Larger batches keep the grid's order, (sequence, kv head) by split:
+        // with hundreds of items per CU the tail is short, and a scan over
+        // every sequence in each workgroup would cost more than it saves.
+        b = blockIdx.x / p.Hkv;
+        kvh = blockIdx.x % p.Hkv;
+        split = blockIdx.y;
+        seq_info(p, b, q_off, L);
+        S = kv_len(p, b);
+        if (split >= decode_items(p, L, S)) return;
+    }
     if (L <= 0) return;
     if (L > p.rq) {
         if (split != 0) return;
@@ -1095,13 +1053,17 @@ Plan make_plan(int batch, int H, int Hkv, int q_hint, int k_hint) {
     pl.decode = q_hint >= 1 && G * q_hint <= 32;
     pl.rq = q_hint;
     pl.ncols = G * q_hint;
-    // Split the key range so that the grid has at least ~2048 workgroups, with
-    // splits as long as that allows (up to 2048 keys): at B=64, Hkv=8 and
-    // kv_len <= 8192, 2048-key splits ran in 194 us against 217 us at 512
-    // (fewer partials to write and merge; the merge kernel is a fixed cost).
+    // Split the key range so that the grid has at least ~512 workgroups (one
+    // per slot of the 256 CUs, two each), with splits as long as that allows:
+    // from 2048 keys down to 512.  Long splits write and merge fewer
+    // partials; at B=64, Hkv=8 and kv_len <= 8192, 2048-key splits ran in
+    // 194 us against 217 us at 512.  Splits shorter than 512 keys cost more
+    // in per-workgroup start-up and merging than they gain in parallelism:
+    // one sequence of 32768 keys took 86 us with 128-key splits, 41 us with
+    // 512; 8 x 4096 keys 55 against 34 us.
     const long long units = static_cast<long long>(batch) * Hkv;
     int split = 2048;
-    while (split > kDecTile && units * ((k_hint + split - 1) / split) < 2048) split >>= 1;
+    while (split > 512 && units * ((k_hint + split - 1) / split) < 512) split >>= 1;
     pl.split_len = split;
     pl.max_splits = k_hint <= 0 ? 1 : (k_hint + split - 1) / split;
     return pl;
