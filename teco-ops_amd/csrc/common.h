@@ -92,6 +92,15 @@ inline unsigned ceil_div(long long a, long long b) {
     return static_cast<unsigned>((a + b - 1) / b);
 }
 
+// Dynamic LDS a workgroup may hold on gfx950, and the amount a kernel gets
+// without raising its limit.
+constexpr size_t kLdsMax = 160 * 1024;
+constexpr size_t kLdsDefault = 64 * 1024;
+
+// Raises a kernel's dynamic-LDS limit to `bytes` (above kLdsDefault) once per
+// process and kernel address; false (with the HIP error cleared) if refused.
+bool reserve_lds(const void *kernel, size_t bytes);
+
 // Compute units of the current device, queried once per device (256 on
 // MI355X; 256 is also the answer when the query fails).
 inline int device_cus() {

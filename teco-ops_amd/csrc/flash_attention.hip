@@ -1075,28 +1075,6 @@ size_t workspace_bytes(const Plan &pl, int batch, int Hkv, int D) {
     return per * D * sizeof(float) + per * 2 * sizeof(float) + 256;
 }
 
-// Raises a kernel's dynamic-LDS limit once per process (per kernel address).
-// The kernels already raised are kept in a fixed table (no heap allocation,
-// so the allocation-free entry point can use it too); past its capacity the
-// attribute is simply set again on every launch.
-bool reserve_lds(const void *kernel, size_t bytes) {
-    static std::mutex mu;
-    static const void *done[256];
-    static int ndone = 0;
-    if (bytes <= 64 * 1024) return true;
-    std::lock_guard<std::mutex> lock(mu);
-    for (int i = 0; i < ndone; ++i)
-        if (done[i] == kernel) return true;
-    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(bytes)) != hipSuccess) {
-        (void)hipGetLastError();
-        TECO_ERROR("flash_attention: cannot reserve %zu bytes of LDS", bytes);
-        return false;
-    }
-    if (ndone < 256) done[ndone++] = kernel;
-    return true;
-}
-
 // Prefill over a grid of ceil(q_hint / QT) query tiles per (b, kv head, head
 // group), then, unless q_hint already bounds every q_len (it is at least the
 // total q length), fa_prefill_rest_kernel for the tiles past the grid.
@@ -1106,8 +1084,8 @@ tecoopsStatus_t launch_prefill(const FaParams &p, const Plan &pl, hipStream_t s)
     auto *kern = &fa_prefill_kernel<T, D, W, HW, QSUB, POW2, TILE>;
     auto *rest = &fa_prefill_rest_kernel<T, D, W, HW, QSUB, POW2, TILE>;
     const size_t lds = prefill_lds_bytes<D, TILE>();
-    if (!reserve_lds(reinterpret_cast<const void *>(kern), lds) ||
-        !reserve_lds(reinterpret_cast<const void *>(rest), lds))
+    if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds) ||
+        !tecoops::reserve_lds(reinterpret_cast<const void *>(rest), lds))
         return TECOOPS_STATUS_INTERNAL_ERROR;
     const int units = p.batch * p.Hkv * (p.G / HW);
     const int tiles = (pl.rq + QT - 1) / QT;
@@ -1134,7 +1112,7 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
     if (pl.decode) {
         const size_t lds = decode_lds_bytes<D>();
         auto *kern = pow2 ? &fa_decode_kernel<T, D, true> : &fa_decode_kernel<T, D, false>;
-        if (!reserve_lds(reinterpret_cast<const void *>(kern), lds)) return TECOOPS_STATUS_INTERNAL_ERROR;
+        if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds)) return TECOOPS_STATUS_INTERNAL_ERROR;
         dim3 grid(p.batch * p.Hkv, pl.max_splits);
         hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, p);
         TECO_CHECK_LAUNCH("flash_attention decode");

@@ -624,7 +624,9 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
                 }
             }
         },
-        // the x chunks reach LDS once the first W loads are in flight
+        // the x chunks reach LDS once the first W loads are in flight; an x
+        // larger than the register-staged part (K > 4096 for 8 rows of x)
+        // copies the rest directly
         [&] {
 #pragma unroll
             for (int j = 0; j < XPT; ++j) {
@@ -634,6 +636,11 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
                     *reinterpret_cast<uint4 *>(xs + xs_chunk(row, c, K)) =
                         row < B ? xr[j] : uint4{0u, 0u, 0u, 0u};
                 }
+            }
+            for (int idx = threadIdx.x + XPT * NW * 64; idx < nxc; idx += NW * 64) {
+                const int row = idx / kx, c = idx - row * kx;
+                *reinterpret_cast<uint4 *>(xs + xs_chunk(row, c, K)) =
+                    row < B ? x[static_cast<long long>(row) * kx + c] : uint4{0u, 0u, 0u, 0u};
             }
             __syncthreads();
         });
@@ -697,7 +704,9 @@ gemv_scalar_kernel(const void *__restrict__ Wv, const uint16_t *__restrict__ sca
     }
 }
 
-constexpr int kMaxLdsBytes = 64 * 1024;
+// x staged in LDS may fill a workgroup's whole LDS (the kernels' limit is
+// raised above the default 64 KiB when it does).
+constexpr long long kMaxLdsBytes = static_cast<long long>(tecoops::kLdsMax);
 
 // Matrix-core path: smallest batch that takes it, row tiles of 16 per
 // workgroup and waves per workgroup.  int8 uses 4 row tiles per x fragment
@@ -724,11 +733,29 @@ constexpr int kRI8 = 2, kCplI8 = 4;
 // groups per wave: 15.0-15.6 us); fp16 with 2, 4, 6, 8, 10, 12 and 16 took
 // 22.0, 22.5, 21.7, 20.8, 20.9, 21.2 and 20.8 us.
 constexpr int kB8RgF16 = 1, kB8CplF16 = 8, kB8RgI8 = 1, kB8CplI8 = 2;
+// Below kB8SmallN rows the grid holds too few waves (4 rows each) to keep HBM
+// busy with 2 int8 steps in flight per lane; 8 then pay.  N = 4096, K = 14336
+// at batch 2 / 4 / 8: 22.1 / 22.6 / 45.0 us with 2, 16.2 / 16.8 / 33.9 with 8;
+// N = 6144, K = 4096 at batch 4: 9.0 against 7.2 us.  At N = 14336 and 28672,
+// batch 8, 8 in flight was slower (12.7 -> 16.3 and 23.6 -> 30.3 us).
+constexpr int kB8SmallN = 8192, kB8CplI8Small = 8;
 constexpr int kB8MaxBatch = 8;
 
-bool b8_fits(int batch, int k, bool i8) {
-    if (batch > kB8MaxBatch || k % (i8 ? 256 : 128) != 0) return false;
-    return static_cast<long long>(batch <= 4 ? 4 : 8) * k * 2 <= kMaxLdsBytes;
+// Rows of x the 4x4x4 path takes per launch for this batch and K (0: the
+// path does not apply): the whole batch when its staged x (4 or 8 rows) fits
+// in LDS, else slices of 4 rows, each launch streaming W once.
+int b8_slice(int batch, int k, bool i8) {
+    if (batch > kB8MaxBatch || k % (i8 ? 256 : 128) != 0) return 0;
+    if (static_cast<long long>(batch <= 4 ? 4 : 8) * k * 2 <= kMaxLdsBytes) return batch;
+    return 4LL * k * 2 <= kMaxLdsBytes ? 4 : 0;
+}
+
+// Rows of x per launch of the VALU path (x [rows, K] staged in LDS): up to 8.
+int vec_slice(int batch, int k) {
+    long long rows = kMaxLdsBytes / (2LL * k);
+    if (rows > 8) rows = 8;
+    if (rows > batch) rows = batch;
+    return static_cast<int>(rows);
 }
 
 // Waves per workgroup of the 4x4x4 path: of 16, 14, 12, 8 and 7, the one that
@@ -750,81 +777,97 @@ int b8_waves(int N, int rows_per_wave) {
     return best;
 }
 
-template <typename T, bool I8, int NCG, int NW>
-void launch_b8_nw(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
+template <typename T, bool I8, int NCG, int NW, int CPL>
+bool launch_b8_nw(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                   hipStream_t s) {
     constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
-    constexpr int CPL = I8 ? kB8CplI8 : kB8CplF16;
-    hipLaunchKernelGGL((gemv_b8_kernel<T, I8, NCG, RG, NW, CPL>),
-                       dim3(tecoops::ceil_div(N, 4 * RG * NW)), dim3(NW * 64), 4 * NCG * K * 2, s,
+    const size_t lds = 4 * NCG * static_cast<size_t>(K) * 2;
+    auto *kern = &gemv_b8_kernel<T, I8, NCG, RG, NW, CPL>;
+    if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds)) return false;
+    hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(N, 4 * RG * NW)), dim3(NW * 64), lds, s,
                        static_cast<const uint4 *>(W), static_cast<const uint16_t *>(sc),
                        static_cast<const uint4 *>(x), static_cast<uint16_t *>(y), N, K, B);
+    return true;
+}
+
+template <typename T, bool I8, int NCG, int CPL>
+bool launch_b8_cpl(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
+                   hipStream_t s) {
+    switch (b8_waves(N, 4 * (I8 ? kB8RgI8 : kB8RgF16))) {
+        case 14: return launch_b8_nw<T, I8, NCG, 14, CPL>(W, sc, x, y, B, N, K, s);
+        case 12: return launch_b8_nw<T, I8, NCG, 12, CPL>(W, sc, x, y, B, N, K, s);
+        case 8: return launch_b8_nw<T, I8, NCG, 8, CPL>(W, sc, x, y, B, N, K, s);
+        case 7: return launch_b8_nw<T, I8, NCG, 7, CPL>(W, sc, x, y, B, N, K, s);
+        default: return launch_b8_nw<T, I8, NCG, 16, CPL>(W, sc, x, y, B, N, K, s);
+    }
 }
 
 template <typename T, bool I8, int NCG>
-void launch_b8_ncg(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
+bool launch_b8_ncg(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                    hipStream_t s) {
-    switch (b8_waves(N, 4 * (I8 ? kB8RgI8 : kB8RgF16))) {
-        case 14: launch_b8_nw<T, I8, NCG, 14>(W, sc, x, y, B, N, K, s); break;
-        case 12: launch_b8_nw<T, I8, NCG, 12>(W, sc, x, y, B, N, K, s); break;
-        case 8: launch_b8_nw<T, I8, NCG, 8>(W, sc, x, y, B, N, K, s); break;
-        case 7: launch_b8_nw<T, I8, NCG, 7>(W, sc, x, y, B, N, K, s); break;
-        default: launch_b8_nw<T, I8, NCG, 16>(W, sc, x, y, B, N, K, s); break;
-    }
+    if (I8 && N < kB8SmallN)
+        return launch_b8_cpl<T, I8, NCG, kB8CplI8Small>(W, sc, x, y, B, N, K, s);
+    return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8 : kB8CplF16>(W, sc, x, y, B, N, K, s);
 }
 
 template <typename T, bool I8>
-void launch_b8(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
+bool launch_b8(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                hipStream_t s) {
-    if (B <= 4)
-        launch_b8_ncg<T, I8, 1>(W, sc, x, y, B, N, K, s);
-    else
-        launch_b8_ncg<T, I8, 2>(W, sc, x, y, B, N, K, s);
+    if (B <= 4) return launch_b8_ncg<T, I8, 1>(W, sc, x, y, B, N, K, s);
+    return launch_b8_ncg<T, I8, 2>(W, sc, x, y, B, N, K, s);
 }
 
 template <typename T, int B>
-void launch16(const void *W, const void *x, void *y, int N, int K, hipStream_t s) {
+bool launch16(const void *W, const void *x, void *y, int N, int K, hipStream_t s) {
     const unsigned grid = tecoops::ceil_div(N, kWaves * kR16);
-    hipLaunchKernelGGL((gemv16_kernel<T, B, kR16, kCpl16, kWaves>), dim3(grid), dim3(kThreads),
+    auto *kern = &gemv16_kernel<T, B, kR16, kCpl16, kWaves>;
+    if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), B * static_cast<size_t>(K) * 2))
+        return false;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads),
                        B * K * 2, s, static_cast<const uint4 *>(W), static_cast<const uint4 *>(x),
                        static_cast<uint16_t *>(y), N, K);
+    return true;
 }
 
 template <int B>
-void launch_i8(const void *W, const void *sc, const void *x, void *y, int N, int K,
+bool launch_i8(const void *W, const void *sc, const void *x, void *y, int N, int K,
                hipStream_t s) {
     const unsigned grid = tecoops::ceil_div(N, kWaves * kRI8);
-    hipLaunchKernelGGL((gemv_i8_kernel<B, kRI8, kCplI8, kWaves>), dim3(grid), dim3(kThreads),
+    auto *kern = &gemv_i8_kernel<B, kRI8, kCplI8, kWaves>;
+    if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), B * static_cast<size_t>(K) * 2))
+        return false;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads),
                        B * K * 2, s, static_cast<const uint4 *>(W),
                        static_cast<const uint16_t *>(sc), static_cast<const uint4 *>(x),
                        static_cast<uint16_t *>(y), N, K);
+    return true;
 }
 
 template <typename T>
-void launch16_b(int B, const void *W, const void *x, void *y, int N, int K, hipStream_t s) {
+bool launch16_b(int B, const void *W, const void *x, void *y, int N, int K, hipStream_t s) {
     switch (B) {
-        case 1: launch16<T, 1>(W, x, y, N, K, s); break;
-        case 2: launch16<T, 2>(W, x, y, N, K, s); break;
-        case 3: launch16<T, 3>(W, x, y, N, K, s); break;
-        case 4: launch16<T, 4>(W, x, y, N, K, s); break;
-        case 5: launch16<T, 5>(W, x, y, N, K, s); break;
-        case 6: launch16<T, 6>(W, x, y, N, K, s); break;
-        case 7: launch16<T, 7>(W, x, y, N, K, s); break;
-        default: launch16<T, 8>(W, x, y, N, K, s); break;
+        case 1: return launch16<T, 1>(W, x, y, N, K, s);
+        case 2: return launch16<T, 2>(W, x, y, N, K, s);
+        case 3: return launch16<T, 3>(W, x, y, N, K, s);
+        case 4: return launch16<T, 4>(W, x, y, N, K, s);
+        case 5: return launch16<T, 5>(W, x, y, N, K, s);
+        case 6: return launch16<T, 6>(W, x, y, N, K, s);
+        case 7: return launch16<T, 7>(W, x, y, N, K, s);
+        default: return launch16<T, 8>(W, x, y, N, K, s);
     }
 }
 
-void launch_i8_b(int B, const void *W, const void *sc, const void *x, void *y, int N, int K,
+bool launch_i8_b(int B, const void *W, const void *sc, const void *x, void *y, int N, int K,
                  hipStream_t s) {
     switch (B) {
-        case 1: launch_i8<1>(W, sc, x, y, N, K, s); break;
-        case 2: launch_i8<2>(W, sc, x, y, N, K, s); break;
-        case 3: launch_i8<3>(W, sc, x, y, N, K, s); break;
-        case 4: launch_i8<4>(W, sc, x, y, N, K, s); break;
-        case 5: launch_i8<5>(W, sc, x, y, N, K, s); break;
-        case 6: launch_i8<6>(W, sc, x, y, N, K, s); break;
-        case 7: launch_i8<7>(W, sc, x, y, N, K, s); break;
-        default: launch_i8<8>(W, sc, x, y, N, K, s); break;
+        case 1: return launch_i8<1>(W, sc, x, y, N, K, s);
+        case 2: return launch_i8<2>(W, sc, x, y, N, K, s);
+        case 3: return launch_i8<3>(W, sc, x, y, N, K, s);
+        case 4: return launch_i8<4>(W, sc, x, y, N, K, s);
+        case 5: return launch_i8<5>(W, sc, x, y, N, K, s);
+        case 6: return launch_i8<6>(W, sc, x, y, N, K, s);
+        case 7: return launch_i8<7>(W, sc, x, y, N, K, s);
+        default: return launch_i8<8>(W, sc, x, y, N, K, s);
     }
 }
 
@@ -840,13 +883,19 @@ extern "C" tecoopsStatus_t tecoopsGemv(tecoopsHandle_t handle, const void *weigh
     using tecoops::dev::bf16;
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
-    if (batch >= kMfmaMinBatch16 && b8_fits(batch, k, false) && tecoops::aligned(weight, 16) &&
-        tecoops::aligned(x, 16)) {
-        if (dataType == TECOOPS_DATA_HALF)
-            launch_b8<f16, false>(weight, nullptr, x, y, batch, n, k, s);
-        else
-            launch_b8<bf16, false>(weight, nullptr, x, y, batch, n, k, s);
-        TECO_CHECK_LAUNCH("gemv");
+    const bool al = tecoops::aligned(weight, 16) && tecoops::aligned(x, 16);
+    const int s8 = batch >= kMfmaMinBatch16 && al ? b8_slice(batch, k, false) : 0;
+    if (s8 > 0) {
+        for (int b0 = 0; b0 < batch; b0 += s8) {
+            const int nb = batch - b0 < s8 ? batch - b0 : s8;
+            const void *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
+            void *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
+            const bool ok = dataType == TECOOPS_DATA_HALF
+                                ? launch_b8<f16, false>(weight, nullptr, xb, yb, nb, n, k, s)
+                                : launch_b8<bf16, false>(weight, nullptr, xb, yb, nb, n, k, s);
+            if (!ok) return TECOOPS_STATUS_INTERNAL_ERROR;
+            TECO_CHECK_LAUNCH("gemv");
+        }
         return TECOOPS_STATUS_SUCCESS;
     }
     if (batch >= kMfmaMinBatch16 && (k % 32) == 0 && tecoops::aligned(weight, 16) &&
@@ -867,16 +916,18 @@ extern "C" tecoopsStatus_t tecoopsGemv(tecoopsHandle_t handle, const void *weigh
         }
         return TECOOPS_STATUS_SUCCESS;
     }
-    const bool vec = (k % 8) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16) &&
-                     8 * k * 2 <= kMaxLdsBytes;
-    if (vec) {
-        // Batches beyond 8 run in slices of 8 rows of x / y.
-        for (int b0 = 0; b0 < batch; b0 += 8) {
-            const int nb = batch - b0 < 8 ? batch - b0 : 8;
+    const int sv = (k % 8) == 0 && al ? vec_slice(batch, k) : 0;
+    if (sv > 0) {
+        // Batches beyond the slice (8 rows of x / y, fewer for long rows) run
+        // in slices.
+        for (int b0 = 0; b0 < batch; b0 += sv) {
+            const int nb = batch - b0 < sv ? batch - b0 : sv;
             const void *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
             void *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
-            if (dataType == TECOOPS_DATA_HALF) launch16_b<f16>(nb, weight, xb, yb, n, k, s);
-            else launch16_b<bf16>(nb, weight, xb, yb, n, k, s);
+            const bool ok = dataType == TECOOPS_DATA_HALF
+                                ? launch16_b<f16>(nb, weight, xb, yb, n, k, s)
+                                : launch16_b<bf16>(nb, weight, xb, yb, n, k, s);
+            if (!ok) return TECOOPS_STATUS_INTERNAL_ERROR;
             TECO_CHECK_LAUNCH("gemv");
         }
         return TECOOPS_STATUS_SUCCESS;
@@ -903,10 +954,17 @@ extern "C" tecoopsStatus_t tecoopsGemvInt8(tecoopsHandle_t handle, const int8_t 
     if (batch <= 0 || n <= 0 || k <= 0) return TECOOPS_STATUS_BAD_PARAM;
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
-    if (batch >= kMfmaMinBatchI8 && b8_fits(batch, k, true) && tecoops::aligned(weight, 16) &&
-        tecoops::aligned(x, 16)) {
-        launch_b8<f16, true>(weight, scales, x, y, batch, n, k, s);
-        TECO_CHECK_LAUNCH("gemv_int8");
+    const bool al = tecoops::aligned(weight, 16) && tecoops::aligned(x, 16);
+    const int s8 = batch >= kMfmaMinBatchI8 && al ? b8_slice(batch, k, true) : 0;
+    if (s8 > 0) {
+        for (int b0 = 0; b0 < batch; b0 += s8) {
+            const int nb = batch - b0 < s8 ? batch - b0 : s8;
+            const void *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
+            void *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
+            if (!launch_b8<f16, true>(weight, scales, xb, yb, nb, n, k, s))
+                return TECOOPS_STATUS_INTERNAL_ERROR;
+            TECO_CHECK_LAUNCH("gemv_int8");
+        }
         return TECOOPS_STATUS_SUCCESS;
     }
     if (batch >= kMfmaMinBatchI8 && (k % 64) == 0 && tecoops::aligned(weight, 16) &&
@@ -923,14 +981,13 @@ extern "C" tecoopsStatus_t tecoopsGemvInt8(tecoopsHandle_t handle, const int8_t 
         }
         return TECOOPS_STATUS_SUCCESS;
     }
-    const bool vec = (k % 16) == 0 && tecoops::aligned(weight, 16) && tecoops::aligned(x, 16) &&
-                     8 * k * 2 <= kMaxLdsBytes;
-    if (vec) {
-        for (int b0 = 0; b0 < batch; b0 += 8) {
-            const int nb = batch - b0 < 8 ? batch - b0 : 8;
+    const int sv = (k % 16) == 0 && al ? vec_slice(batch, k) : 0;
+    if (sv > 0) {
+        for (int b0 = 0; b0 < batch; b0 += sv) {
+            const int nb = batch - b0 < sv ? batch - b0 : sv;
             const void *xb = static_cast<const uint16_t *>(x) + static_cast<long long>(b0) * k;
             void *yb = static_cast<uint16_t *>(y) + static_cast<long long>(b0) * n;
-            launch_i8_b(nb, weight, scales, xb, yb, n, k, s);
+            if (!launch_i8_b(nb, weight, scales, xb, yb, n, k, s)) return TECOOPS_STATUS_INTERNAL_ERROR;
             TECO_CHECK_LAUNCH("gemv_int8");
         }
         return TECOOPS_STATUS_SUCCESS;

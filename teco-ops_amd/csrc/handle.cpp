@@ -7,6 +7,8 @@
 // stream it runs split-KV attention on, and descriptors free their >8-dim
 // arrays.  Create/Destroy of a handle that never
 // ran an op make no HIP call.
+#include <mutex>
+
 #include "common.h"
 
 #include <cstdlib>
@@ -187,6 +189,27 @@ tecoopsStatus_t tecoopsMorton3DInvert(tecoopsHandle_t handle, const int *indices
 }  // extern "C"
 
 namespace tecoops {
+
+// The kernels already raised are kept in a fixed table (no heap allocation, so
+// the allocation-free entry points can use it too); past its capacity the
+// attribute is simply set again on every launch.
+bool reserve_lds(const void *kernel, size_t bytes) {
+    static std::mutex mu;
+    static const void *done[256];
+    static int ndone = 0;
+    if (bytes <= kLdsDefault) return true;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < ndone; ++i)
+        if (done[i] == kernel) return true;
+    if (bytes > kLdsMax || hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               static_cast<int>(bytes)) != hipSuccess) {
+        (void)hipGetLastError();
+        TECO_ERROR("cannot reserve %zu bytes of LDS for a kernel", bytes);
+        return false;
+    }
+    if (ndone < 256) done[ndone++] = kernel;
+    return true;
+}
 
 tecoopsStatus_t handle_scratch(tecoopsHandle_t handle, size_t bytes, void **out) {
     if (bytes == 0) bytes = 256;

@@ -543,6 +543,35 @@ def test_gemv_int8(B):
     assert_close(got, ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2, what=f"gemv_int8 B={B}")
 
 
+@pytest.mark.parametrize("B,K", [(1, 14336), (2, 14336), (4, 14336), (5, 14336), (8, 14336),
+                                 (4, 20480), (3, 24576), (1, 40960)])
+@pytest.mark.parametrize("i8", [False, True], ids=["fp16", "int8"])
+def test_gemv_long_rows(B, K, i8):
+    """Rows longer than 64 KiB of staged x: the 4x4x4 path stages up to the
+    workgroup's whole LDS (4 x 20480 x 2 bytes is exactly 160 KiB) and takes
+    batches above 4 in slices of 4 when 8 rows do not fit; the VALU path
+    stages up to 160 KiB of x per launch; 3 x 24576 falls to the 16x16x32
+    path (no staging)."""
+    r = rng(700 + B + K // 1024 + (50 if i8 else 0))
+    N = 1000
+    x = bits(r.standard_normal((B, K)))
+    y = torch.empty((B, N), dtype=torch.float16, device="cuda")
+    if i8:
+        W = r.integers(-127, 128, (N, K), dtype=np.int8)
+        s = bits(r.uniform(0.001, 0.01, N))
+        ref = orc.gemv_int8(W, s, x)
+        tecoops.gemv_int8(dev(W), dev(s), dev(x), y)
+        torch.cuda.synchronize()
+        assert_close(as_f32(y), ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2,
+                     what=f"gemv_int8 {B}x{N}x{K}")
+    else:
+        W = bits(r.normal(0, 0.02, (N, K)))
+        ref = orc.gemv(W, x)
+        tecoops.gemv(dev(W), dev(x), y)
+        torch.cuda.synchronize()
+        assert_close(as_f32(y), ref, what=f"gemv {B}x{N}x{K}")
+
+
 @pytest.mark.parametrize("K", [32, 224, 1248, 2080])
 @pytest.mark.parametrize("dt", [orc.HALF, orc.BF16])
 def test_gemv_matrix_core_ragged_k(K, dt):
