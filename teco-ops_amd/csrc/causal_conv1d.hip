@@ -314,6 +314,60 @@ __global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {
     }
 }
 
+// ------------------------------------------------------- short sequences
+
+// Decode steps and short chunks (a few tokens per sequence): one thread per
+// (sequence, channel), channels fastest, so that the conv-state rows and a
+// [tokens, dim] x are read and written coalesced; the thread walks its
+// sequence's tokens with the window in registers.  Same arithmetic order as
+// the other kernels (oldest window element first, bias, then the activation).
+template <int W, bool SILU>
+__global__ void __launch_bounds__(256) conv1d_short_kernel(ConvArgs a) {
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= static_cast<long long>(a.batch) * a.dim) return;
+    const int b = static_cast<int>(i / a.dim), d = static_cast<int>(i % a.dim);
+    long long len, xoff, ooff;
+    if (a.qsl != nullptr) {
+        const long long s0 = a.qsl[b];
+        len = a.qsl[b + 1] - s0;
+        xoff = s0 * a.xs;
+        ooff = s0 * a.os;
+    } else {
+        len = a.seq_len;
+        xoff = b * a.xb;
+        ooff = b * a.ob;
+    }
+    const int cidx = a.cidx ? a.cidx[b] : b;
+    if (cidx == a.pad_slot_id || len <= 0) return;
+    const uint16_t *xr = a.x + xoff + d * a.xd;
+    uint16_t *outr = a.out + ooff + d * a.od;
+    const bool use_state =
+        a.state != nullptr && (a.api_mode == 1 || (a.hinit != nullptr && a.hinit[b] != 0));
+    uint16_t *st = a.state ? a.state + static_cast<long long>(cidx) * a.state_stride + d : nullptr;
+    float wv[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
+    const float bv = a.bias ? h2f(a.bias[d]) : 0.0f;
+    uint16_t raw[W - 1];  // the last W-1 inputs (state or zeros before the first token)
+#pragma unroll
+    for (int k = 0; k < W - 1; ++k) raw[k] = use_state ? st[static_cast<long long>(k) * a.dim] : 0;
+    for (long long t = 0; t < len; ++t) {
+        const uint16_t xv = xr[t * a.xs];
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < W - 1; ++k) acc += h2f(raw[k]) * wv[k];
+        acc += h2f(xv) * wv[W - 1];
+        outr[t * a.os] = f2h(act<SILU>(acc + bv));
+#pragma unroll
+        for (int k = 0; k < W - 2; ++k) raw[k] = raw[k + 1];
+        raw[W - 2] = xv;
+    }
+    if (st != nullptr) {
+#pragma unroll
+        for (int k = 0; k < W - 1; ++k) st[static_cast<long long>(k) * a.dim] = raw[k];
+    }
+}
+
 // ------------------------------------------------ channel-contiguous tokens
 
 constexpr int kTokChunk = 8;    // tokens per lane (4 measured alike, 16 slower)
@@ -572,6 +626,12 @@ bool tokens_layout(const ConvArgs &a) {
     return true;
 }
 
+// Mean sequence length up to which conv1d_short_kernel runs.  [dim, tokens]
+// x, dim 4096, 64 sequences: 1 token 134 -> 8 us against the row kernel,
+// 16 tokens 138 -> 35 us, 32 tokens 146 -> 127 us, 64 tokens 163 -> 440 us
+// (the per-thread token walk is one dependent round trip per token).
+constexpr long long kShortLen = 32;
+
 template <int W, bool SILU>
 void launch(const ConvArgs &a0, bool seq_contig, long long max_len, hipStream_t s) {
     ConvArgs a = a0;
@@ -585,6 +645,15 @@ void launch(const ConvArgs &a0, bool seq_contig, long long max_len, hipStream_t 
         const long long per_xcd = (nitems + 7) / 8;
         hipLaunchKernelGGL((conv1d_tokens_kernel<W, SILU>), dim3(static_cast<unsigned>(8 * per_xcd)),
                            dim3(256), 0, s, a, nitems, per_xcd, nslabs);
+        return;
+    }
+    // mean tokens per sequence: the whole axis over the batch with
+    // query_start_loc, seq_len without
+    const long long mean_len = a.qsl ? (max_len + a.batch - 1) / a.batch : a.seq_len;
+    if (mean_len <= kShortLen) {
+        const unsigned grid =
+            static_cast<unsigned>(tecoops::ceil_div(static_cast<long long>(a.batch) * a.dim, 256));
+        hipLaunchKernelGGL((conv1d_short_kernel<W, SILU>), dim3(grid), dim3(256), 0, s, a);
         return;
     }
     if (seq_contig) {

@@ -398,6 +398,51 @@ def test_causal_conv1d_reference_layout_long_varlen():
     assert np.array_equal(host_bits(st_dev), st_ref)
 
 
+@pytest.mark.parametrize("W", [2, 3, 4])
+@pytest.mark.parametrize("case", ["decode", "short_varlen"])
+def test_causal_conv1d_short_sequences(W, case):
+    """Reference torch layout [dim, tokens] with short sequences (mean <= 32
+    tokens: the per-(sequence, channel) kernel): a decode step of 70
+    sequences of one token, and a chunked mix of 1..40 tokens; shuffled cache
+    slots, sequences without initial state and one pad slot (its output and
+    state untouched).  Output and state against the oracle; the state is
+    bit-exact."""
+    r = rng(950 + W + (0 if case == "decode" else 10))
+    dim = 200
+    lens = [1] * 70 if case == "decode" else r.integers(1, 41, 37).tolist()
+    B, total = len(lens), sum(lens)
+    x = bits(r.standard_normal((dim, total)))
+    w = bits(r.standard_normal((W, dim)))
+    st = bits(r.standard_normal((B + 3, W - 1, dim)))
+    qsl = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cidx = r.permutation(B + 3)[:B].astype(np.int32)
+    cidx[5] = -7  # pad slot
+    hinit = (r.random(B) < 0.7).astype(np.int8)
+    st_ref = st.copy()
+    ref = orc.causal_conv1d(x, w, conv_state=st_ref, query_start_loc=qsl, cache_indices=cidx,
+                            has_initial_state=hinit, pad_slot_id=-7, layout="dl")
+    out = torch.zeros((dim, total), dtype=torch.float16, device="cuda")
+    st_dev = dev(st)
+    tecoops.causal_conv1d_fn_torch(out, st_dev, dev(x), dev(w), dev(qsl), dev(cidx), dev(hinit),
+                                   -7)
+    torch.cuda.synchronize()
+    assert_close(as_f32(out), ref, what=f"conv short {case} W={W}")
+    assert np.array_equal(host_bits(st_dev), st_ref)
+
+
+def test_causal_conv1d_short_rows_bdl():
+    """[B, dim, L] with L = 16 (the per-(sequence, channel) kernel), bias and
+    SiLU, no state."""
+    r = rng(970)
+    xb = bits(r.standard_normal((40, 96, 16)))
+    wb = bits(r.standard_normal((96, 4)))
+    bb = bits(r.standard_normal(96))
+    ob = torch.empty((40, 96, 16), dtype=torch.float16, device="cuda")
+    tecoops.causal_conv1d(dev(xb), dev(wb), dev(bb), ob)
+    torch.cuda.synchronize()
+    assert_close(as_f32(ob), orc.causal_conv1d(xb, wb, bias=bb, layout="bdl"), what="conv bdl L=16")
+
+
 def _conv_c_api(x, w, st, qsl, cidx, hinit, pad, api_mode, W):
     """tecoopsCausalConv1d on token-major x [tokens, dim] (the reference C
     layout); returns out and the updated state as numpy bits."""
