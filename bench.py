@@ -23,7 +23,7 @@ this steady state an op's HBM traffic per launch equals its algorithmic bytes
 (its own dirty outputs are written back during later launches).  Per-op kernel
 time: K back-to-back launches of the op between one pair of torch.cuda events
 on the stream the ops are enqueued on (tecoops binds the current torch
-stream), divided by K, right after a warm-up of at least W launches and 30 ms
+stream), divided by K, right after a warm-up of at least W launches and 200 ms
 of the same op.  Beside it, `us_median20` is the median of 20 more launches
 of the op, each between its own pair of events (the extra event markers
 between launches can add a little to each).
@@ -87,7 +87,10 @@ def seeded_bits(rng, shape, kind="normal", scale=1.0, lo=0.0, hi=1.0, dtype="f16
 
 
 ROTATE_BYTES = 1 << 30   # rotating working set per op: 4x the 256 MiB MALL
-WARM_S = 0.03            # minimum warm-up per op, seconds of its own launches
+# Minimum warm-up per op, seconds of its own launches.  FA prefill after 30 ms
+# still ran its first timed launches slow (mean 579 us, median of the later
+# launches 567 us); after 200 ms the mean and the median agree (569 us).
+WARM_S = 0.2
 
 
 def copies_for(ws_bytes, limit=16):
