@@ -314,6 +314,149 @@ __global__ void __launch_bounds__(256) conv1d_rows_kernel(ConvArgs a) {
     }
 }
 
+// --------------------------------------------------- short rows, grouped
+
+// Token-contiguous rows of a few hundred tokens at most: the wave's 64 lanes
+// hold 64 / G rows side by side, G lanes per row (segments of 8G tokens), so
+// that a wave is not mostly idle on a short row.  Within each group of G
+// lanes this is conv1d_rows_kernel: the W-1 inputs before a lane's tokens
+// come from lane l-1 of its group (a shuffle of width G), from the group's
+// last lane in the previous segment, or from the carried values / the prefix
+// at the start of the row.  Rows of one wave can differ in length (varlen
+// batches): the wave walks the longest and every lane guards its own tokens.
+template <int W, bool SILU, int G>
+__global__ void __launch_bounds__(256) conv1d_rows_group_kernel(ConvArgs a) {
+    constexpr int CH = 8, SEG = G * CH, R = 64 / G;
+    const int lane = threadIdx.x & 63, gl = lane % G;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const long long nrows = static_cast<long long>(a.batch) * a.dim;
+    const long long r = (static_cast<long long>(blockIdx.x) * 4 + wave) * R + lane / G;
+    int b = 0, d = 0, cidx = 0;
+    long long len = 0, xoff = 0, ooff = 0;
+    if (r < nrows) {
+        b = static_cast<int>(r / a.dim);
+        d = static_cast<int>(r % a.dim);
+        if (a.qsl != nullptr) {
+            const long long s0 = a.qsl[b];
+            len = a.qsl[b + 1] - s0;
+            xoff = s0 * a.xs;
+            ooff = s0 * a.os;
+        } else {
+            len = a.seq_len;
+            xoff = b * a.xb;
+            ooff = b * a.ob;
+        }
+        cidx = a.cidx ? a.cidx[b] : b;
+        if (cidx == a.pad_slot_id || len < 0) len = 0;
+    }
+    long long mlen = len;  // the wave's longest row
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mlen = max(mlen, static_cast<long long>(__shfl_xor(mlen, o, 64)));
+    if (mlen <= 0) return;
+    const uint16_t *xr = a.x + xoff + d * a.xd;
+    uint16_t *outr = a.out + ooff + d * a.od;
+    const bool use_state = len > 0 && a.state != nullptr &&
+                           (a.api_mode == 1 || (a.hinit != nullptr && a.hinit[b] != 0));
+    uint16_t *st = len > 0 && a.state ? a.state + static_cast<long long>(cidx) * a.state_stride + d
+                                      : nullptr;
+    const bool vec_row = tecoops::aligned(xr, 16) && tecoops::aligned(outr, 16);
+    float wv[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) wv[k] = h2f(a.w[static_cast<long long>(d) * a.wd + k * a.ww]);
+    const float bv = a.bias ? h2f(a.bias[d]) : 0.0f;
+    uint16_t prefix[W - 1];
+#pragma unroll
+    for (int k = 0; k < W - 1; ++k) prefix[k] = use_state ? st[static_cast<long long>(k) * a.dim] : 0;
+    float carry[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < W - 1; ++k) carry[3 - (W - 1) + k] = h2f(prefix[k]);
+
+    for (long long g0 = 0; g0 < mlen; g0 += kSegs * SEG) {
+        uint32_t dw[kSegs][4];
+#pragma unroll
+        for (int u = 0; u < kSegs; ++u) {
+            const long long t0 = g0 + u * SEG + gl * CH;
+            if (vec_row && t0 + CH <= len) {
+                const uint4 q = ld_stream(reinterpret_cast<const uint4 *>(xr + t0));
+                dw[u][0] = q.x; dw[u][1] = q.y; dw[u][2] = q.z; dw[u][3] = q.w;
+            } else {
+                uint16_t e[CH];
+#pragma unroll
+                for (int j = 0; j < CH; ++j) e[j] = (t0 + j < len) ? xr[t0 + j] : 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    dw[u][j] = e[2 * j] | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kSegs; ++u) {
+            const long long t0 = g0 + u * SEG + gl * CH;
+            // all lanes take part in the shuffles; the group's first lane then
+            // takes the previous segment's last lane, or the carry
+            const uint32_t p2 = __shfl_up(dw[u][2], 1, G);
+            const uint32_t p3 = __shfl_up(dw[u][3], 1, G);
+            const uint32_t q2 = u > 0 ? __shfl(dw[u > 0 ? u - 1 : 0][2], G - 1, G) : 0u;
+            const uint32_t q3 = u > 0 ? __shfl(dw[u > 0 ? u - 1 : 0][3], G - 1, G) : 0u;
+            float prev[3] = {hi<f16>(p2), lo<f16>(p3), hi<f16>(p3)};
+            if (gl == 0) {
+                if (u == 0) {
+                    prev[0] = carry[0]; prev[1] = carry[1]; prev[2] = carry[2];
+                } else {
+                    prev[0] = hi<f16>(q2); prev[1] = lo<f16>(q3); prev[2] = hi<f16>(q3);
+                }
+            }
+            if (t0 >= len) continue;
+            float win[W - 1 + CH];
+#pragma unroll
+            for (int k = 0; k < W - 1; ++k) win[k] = prev[3 - (W - 1) + k];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                win[W - 1 + 2 * j] = lo<f16>(dw[u][j]);
+                win[W - 1 + 2 * j + 1] = hi<f16>(dw[u][j]);
+            }
+            float o[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < W; ++k) acc += win[j + k] * wv[k];
+                o[j] = act<SILU>(acc + bv);
+            }
+            if (vec_row && t0 + CH <= len) {
+                uint4 q;
+                q.x = pack_h2(o[0], o[1]);
+                q.y = pack_h2(o[2], o[3]);
+                q.z = pack_h2(o[4], o[5]);
+                q.w = pack_h2(o[6], o[7]);
+                st_stream(reinterpret_cast<uint4 *>(outr + t0), q);
+            } else {
+#pragma unroll
+                for (int j = 0; j < CH; ++j)
+                    if (t0 + j < len) outr[t0 + j] = f2h(o[j]);
+            }
+        }
+        // the next group of segments starts at g0 + kSegs * SEG only where this
+        // one was full, and then its last three tokens are the group's last lane's
+        const uint32_t c2 = __shfl(dw[kSegs - 1][2], G - 1, G);
+        const uint32_t c3 = __shfl(dw[kSegs - 1][3], G - 1, G);
+        carry[0] = hi<f16>(c2); carry[1] = lo<f16>(c3); carry[2] = hi<f16>(c3);
+    }
+    if (gl == 0 && st != nullptr) {
+        uint16_t ns[W - 1];
+#pragma unroll
+        for (int k = 0; k < W - 1; ++k) {
+            const long long src = len - (W - 1) + k;
+            uint16_t old = 0;  // prefix[W - 1 + src] without a dynamic index
+#pragma unroll
+            for (int m = 0; m < W - 1; ++m)
+                if (m == W - 1 + src) old = prefix[m];
+            ns[k] = src >= 0 ? xr[src] : old;
+        }
+#pragma unroll
+        for (int k = 0; k < W - 1; ++k) st[static_cast<long long>(k) * a.dim] = ns[k];
+    }
+}
+
 // ------------------------------------------------------- short sequences
 
 // Decode steps and short chunks (a few tokens per sequence): one thread per
@@ -626,11 +769,14 @@ bool tokens_layout(const ConvArgs &a) {
     return true;
 }
 
-// Mean sequence length up to which conv1d_short_kernel runs.  [dim, tokens]
-// x, dim 4096, 64 sequences: 1 token 134 -> 8 us against the row kernel,
-// 16 tokens 138 -> 35 us, 32 tokens 146 -> 127 us, 64 tokens 163 -> 440 us
-// (the per-thread token walk is one dependent round trip per token).
-constexpr long long kShortLen = 32;
+// Mean sequence length up to which conv1d_short_kernel runs rather than the
+// grouped-row kernel: its per-thread token walk is one dependent round trip
+// per token, and coalesced only when neighbouring channels are close in
+// memory.  dim 4096, 64 sequences, short / 16 rows per wave: [B, dim, L]
+// with 8 tokens 8.4 / 12.4 us, 12 tokens 10.5 / 15.0 us; [dim, tokens]
+// (channels a whole token axis apart) with 4 tokens 10.8 / 10.7 us, 8 tokens
+// 18.3 / 15.7 us.  One token: 8 us against 134 us with one row per wave.
+constexpr long long kShortLenNear = 12, kShortLenFar = 4;
 
 template <int W, bool SILU>
 void launch(const ConvArgs &a0, bool seq_contig, long long max_len, hipStream_t s) {
@@ -650,10 +796,26 @@ void launch(const ConvArgs &a0, bool seq_contig, long long max_len, hipStream_t 
     // mean tokens per sequence: the whole axis over the batch with
     // query_start_loc, seq_len without
     const long long mean_len = a.qsl ? (max_len + a.batch - 1) / a.batch : a.seq_len;
-    if (mean_len <= kShortLen) {
+    if (mean_len <= (a.xd <= 64 ? kShortLenNear : kShortLenFar)) {
         const unsigned grid =
             static_cast<unsigned>(tecoops::ceil_div(static_cast<long long>(a.batch) * a.dim, 256));
         hipLaunchKernelGGL((conv1d_short_kernel<W, SILU>), dim3(grid), dim3(256), 0, s, a);
+        return;
+    }
+    if (seq_contig && mean_len <= 256) {
+        // short rows: 16, 8, 4 or 2 rows per wave (segments of 32, 64, 128
+        // and 256 tokens)
+        const long long rows = static_cast<long long>(a.batch) * a.dim;
+        const int rpw = mean_len <= 32 ? 16 : mean_len <= 64 ? 8 : mean_len <= 128 ? 4 : 2;
+        const unsigned grid = static_cast<unsigned>(tecoops::ceil_div(rows, 4LL * rpw));
+        if (rpw == 16)
+            hipLaunchKernelGGL((conv1d_rows_group_kernel<W, SILU, 4>), dim3(grid), dim3(256), 0, s, a);
+        else if (rpw == 8)
+            hipLaunchKernelGGL((conv1d_rows_group_kernel<W, SILU, 8>), dim3(grid), dim3(256), 0, s, a);
+        else if (rpw == 4)
+            hipLaunchKernelGGL((conv1d_rows_group_kernel<W, SILU, 16>), dim3(grid), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((conv1d_rows_group_kernel<W, SILU, 32>), dim3(grid), dim3(256), 0, s, a);
         return;
     }
     if (seq_contig) {

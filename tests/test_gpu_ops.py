@@ -430,6 +430,49 @@ def test_causal_conv1d_short_sequences(W, case):
     assert np.array_equal(host_bits(st_dev), st_ref)
 
 
+@pytest.mark.parametrize("W", [2, 3, 4])
+@pytest.mark.parametrize("lo,hi", [(8, 40), (20, 110), (60, 200), (100, 420)])
+def test_causal_conv1d_grouped_rows_varlen(W, lo, hi):
+    """Reference torch layout [dim, tokens] with sequences of lo..hi tokens
+    (mean 13..256: several rows per wave, 4 to 32 lanes each, rows of one
+    wave of different lengths and mostly misaligned), shuffled cache slots,
+    sequences without initial state and one pad slot."""
+    r = rng(980 + W + lo)
+    dim = 72
+    lens = r.integers(lo, hi + 1, 23).tolist()
+    B, total = len(lens), sum(lens)
+    x = bits(r.standard_normal((dim, total)))
+    w = bits(r.standard_normal((W, dim)))
+    st = bits(r.standard_normal((B + 2, W - 1, dim)))
+    qsl = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cidx = r.permutation(B + 2)[:B].astype(np.int32)
+    cidx[3] = -7
+    hinit = (r.random(B) < 0.7).astype(np.int8)
+    st_ref = st.copy()
+    ref = orc.causal_conv1d(x, w, conv_state=st_ref, query_start_loc=qsl, cache_indices=cidx,
+                            has_initial_state=hinit, pad_slot_id=-7, layout="dl")
+    out = torch.zeros((dim, total), dtype=torch.float16, device="cuda")
+    st_dev = dev(st)
+    tecoops.causal_conv1d_fn_torch(out, st_dev, dev(x), dev(w), dev(qsl), dev(cidx), dev(hinit),
+                                   -7)
+    torch.cuda.synchronize()
+    assert_close(as_f32(out), ref, what=f"conv grouped rows {lo}..{hi} W={W}")
+    assert np.array_equal(host_bits(st_dev), st_ref)
+
+
+@pytest.mark.parametrize("L", [13, 24, 40, 64, 100, 200, 256])
+def test_causal_conv1d_grouped_rows_bdl(L):
+    """[B, dim, L] with 13..256 tokens per row, bias and SiLU, no state."""
+    r = rng(990 + L)
+    xb = bits(r.standard_normal((9, 50, L)))
+    wb = bits(r.standard_normal((50, 4)))
+    bb = bits(r.standard_normal(50))
+    ob = torch.empty((9, 50, L), dtype=torch.float16, device="cuda")
+    tecoops.causal_conv1d(dev(xb), dev(wb), dev(bb), ob)
+    torch.cuda.synchronize()
+    assert_close(as_f32(ob), orc.causal_conv1d(xb, wb, bias=bb, layout="bdl"), what=f"conv bdl L={L}")
+
+
 def test_causal_conv1d_short_rows_bdl():
     """[B, dim, L] with L = 16 (the per-(sequence, channel) kernel), bias and
     SiLU, no state."""
