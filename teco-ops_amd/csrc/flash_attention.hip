@@ -616,7 +616,7 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
 // W >= 12 asks for 3 waves per SIMD (168 VGPRs); head sizes above 128 one
 // workgroup per CU (their LDS tiles allow no more); else 2.
 template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
-__global__ void __launch_bounds__(W * 64, W >= 12 ? 3 : (D > 128 ? 1 : 2))
+__global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 ? 1 : 2))
 fa_prefill_kernel(FaParams p) {
     constexpr int QT = 32 * QSUB * (W / HW);
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -643,7 +643,7 @@ fa_prefill_kernel(FaParams p) {
 // that fa_prefill_kernel has no loop around its tile (values hoisted out of
 // a loop would stay live across the tile and cost registers).
 template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
-__global__ void __launch_bounds__(W * 64, W >= 12 ? 3 : (D > 128 ? 1 : 2))
+__global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 ? 1 : 2))
 fa_prefill_rest_kernel(FaParams p, int first_tile) {
     constexpr int QT = 32 * QSUB * (W / HW);
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -1122,8 +1122,19 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
         return TECOOPS_STATUS_SUCCESS;
     }
     if constexpr (D == 128) {
-        // the uniform-page loader: 12 waves (3 per SIMD), 96-key tiles
-        if (pow2) return prefill_hw<T, D, 12, 1, true, 96>(p, pl, s);
+        // the uniform-page loader.  Long query ranges: 12 waves (3 per SIMD)
+        // over 96 query rows and 96-key tiles.  Up to 1024 query rows (short
+        // prompts, chunks over a cached context): 4 waves over 32 rows and
+        // 32-key tiles, three workgroups per CU, which wastes fewer masked
+        // rows and hides each workgroup's start-up behind the others.  bf16,
+        // H32 Hkv8, µs 12-wave / 4-wave: 64 x 16 rows over 4096 keys 446 /
+        // 278, 64 x 32 408 / 249, 16 x 256 384 / 354, 8 x 512 341 / 327,
+        // prefill 16 x 1024 220 / 206, 4 x 4096 643 / 689, 1 x 16384 2162 /
+        // 2370.
+        if (pow2) {
+            if (pl.rq <= 1024) return prefill_hw<T, D, 4, 1, true, 32>(p, pl, s);
+            return prefill_hw<T, D, 12, 1, true, 96>(p, pl, s);
+        }
     }
     return pow2 ? prefill_hw<T, D, 4, 1, true>(p, pl, s) : prefill_hw<T, D, 4, 1, false>(p, pl, s);
 }

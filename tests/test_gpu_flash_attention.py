@@ -341,6 +341,21 @@ def test_prefill_rows_past_max_seqlen_q():
         assert_close(got, ref, what=f"prefill max_q={max_q}")
 
 
+@pytest.mark.parametrize("dt", [orc.HALF, orc.BF16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("H,Hkv", [(8, 2), (6, 3), (5, 5)])
+def test_prefill_long_query_ranges(dt, H, Hkv):
+    """Query ranges above 1024 rows take the 12-wave kernel (96-row tiles,
+    4, 2 or 1 heads per GQA group): ragged lengths, chunks with a cached
+    prefix (kv longer than q), a sequence shorter than one tile, and a
+    max_seqlen_q hint below the longest range (tiles past the grid)."""
+    q_lens, kv = [1100, 1537, 40, 1300], [1100, 2000, 900, 1300]
+    q, kc, vc, bt = make_inputs(36 + H, H, Hkv, 128, 16, q_lens, kv, dtype=dt)
+    ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=dt)
+    for max_q in (None, 1100):
+        got = run_gpu(q, kc, vc, bt, q_lens, kv, dt, max_q=max_q)
+        assert_close(got, ref, what=f"long query ranges H={H} Hkv={Hkv} max_q={max_q}")
+
+
 def test_kv_len_clamped_to_block_table():
     """kv_len past block_table_dim * block_size (the reference's precondition,
     flash_attention.scpp:190) reads no block-table entry past the row: the
