@@ -195,13 +195,16 @@ struct TileLoader {
     __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
                                          int j0, int kv_limit) {
         const int tid = threadIdx.x;
+        // All page lookups first, then all K/V loads: a load whose address
+        // waits on a block-table read interleaved with the K/V loads would
+        // wait for every K/V load issued before it (loads complete in order),
+        // one round trip per row.
+        long long ko[KCH], vo[VPT][4];
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
             const int task = tid + i * NT;
             bool ok;
-            const long long o = row_offset<D, POW2>(p, bt_row, head_off, j0 + task / CPR,
-                                                    kv_limit, ok);
-            k[i] = load16<STREAM>(p.kc + o + (task % CPR) * 8);
+            ko[i] = row_offset<D, POW2>(p, bt_row, head_off, j0 + task / CPR, kv_limit, ok);
         }
         // Invalid V rows are zeroed in store(), so the wave does not wait for
         // the loads here.
@@ -210,15 +213,23 @@ struct TileLoader {
         for (int i = 0; i < VPT; ++i) {
             const int task = tid + i * NT;
             if (VTASKS % NT != 0 && task >= VTASKS) continue;
-            const int rg = task % (TILE / 4), cg = task / (TILE / 4);
+            const int rg = task % (TILE / 4);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 bool ok;
-                const long long o = row_offset<D, POW2>(p, bt_row, head_off, j0 + 4 * rg + r,
-                                                        kv_limit, ok);
-                v[i][r] = load16<STREAM>(p.vc + o + cg * 8);
+                vo[i][r] = row_offset<D, POW2>(p, bt_row, head_off, j0 + 4 * rg + r, kv_limit, ok);
                 vok |= (ok ? 1u : 0u) << (4 * i + r);
             }
+        }
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) k[i] = load16<STREAM>(p.kc + ko[i] + ((tid + i * NT) % CPR) * 8);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int task = tid + i * NT;
+            if (VTASKS % NT != 0 && task >= VTASKS) continue;
+            const int cg = task / (TILE / 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[i][r] = load16<STREAM>(p.vc + vo[i][r] + cg * 8);
         }
     }
 
