@@ -370,7 +370,7 @@ def test_kv_len_clamped_to_block_table():
 # head sizes the reference takes (BK = size_per_head in 32-column slabs,
 # flash_attention.scpp:188, :347-348)
 
-@pytest.mark.parametrize("D", [32, 96, 160, 192])
+@pytest.mark.parametrize("D", [32, 64, 96, 160, 192])
 @pytest.mark.parametrize("dt", [orc.HALF, orc.BF16], ids=["fp16", "bf16"])
 def test_head_sizes(D, dt):
     for name, H, Hkv, bs, q_lens, kv_lens in (
@@ -380,6 +380,19 @@ def test_head_sizes(D, dt):
         case = dict(name=f"{name} D={D}", H=H, Hkv=Hkv, D=D, bs=bs, q_lens=q_lens,
                     kv_lens=kv_lens)
         check(case, dt, seed=D + len(name))
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32, 5])
+def test_head_size_64_block_sizes(bs):
+    """D = 64 with block sizes 8 (the page-uniform loader's V groups of 16
+    rows then span two cache blocks), 16, 32 and 5 (the generic loader):
+    prefill with a cached prefix, decode and a chunk."""
+    for name, H, Hkv, q_lens, kv_lens in (("prefill", 8, 2, [130, 77], [300, 77]),
+                                          ("decode", 16, 4, [1, 1, 1], [3, 700, 2500]),
+                                          ("chunk", 8, 4, [33, 20], [90, 20])):
+        case = dict(name=f"D=64 bs={bs} {name}", H=H, Hkv=Hkv, D=64, bs=bs, q_lens=q_lens,
+                    kv_lens=kv_lens)
+        check(case, orc.BF16, seed=bs + len(name))
 
 
 # ------------------------------------------------------------------------
