@@ -472,6 +472,97 @@ struct PagedLoader64 {
     }
 };
 
+// The same scheme for D = 96 (12 chunks of 16 bytes per row): a K load
+// instruction covers 4 aligned rows on lanes 0-47 and a V instruction 8
+// aligned rows (lane l: rows 2*(l%4) + {0,1}, column block l/4) on lanes
+// 0-47; lanes 48-63 repeat lane 47's load and store nothing.
+template <int TILE, int W, bool STREAM = false>
+struct PagedLoader96 {
+    static constexpr int D = 96;
+    static constexpr int KP = D + 8;
+    static constexpr int VP = TILE + 4;
+    static constexpr int ELEMS = TILE * KP + D * VP;
+    static constexpr int RW = TILE / W;     // rows per wave
+    static constexpr int KI = RW / 4;       // K load instructions per wave
+    static constexpr int VI = RW / 8;       // V load instruction pairs per wave
+    static_assert(RW % 8 == 0, "each wave stages whole 8-row groups");
+    u32x4 k[KI];
+    u32x4 v[VI][2];
+    uint32_t vok;     // bit 2i+j: V row of v[i][j] is below kv_limit
+    int pg[KI + VI];  // cache block ids of the next load()'s row groups (uniform)
+
+    __device__ __forceinline__ void prefetch(const FaParams &p, const int *bt_row, int j0,
+                                             int kv_limit) {
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < KI; ++i)
+            pg[i] = PagedLoader128<TILE, W, STREAM>::group_page(p, bt_row, j0 + w * RW + 4 * i,
+                                                                kv_limit);
+#pragma unroll
+        for (int i = 0; i < VI; ++i)
+            pg[KI + i] = PagedLoader128<TILE, W, STREAM>::group_page(p, bt_row,
+                                                                     j0 + w * RW + 8 * i, kv_limit);
+    }
+
+    static __device__ __forceinline__ long long group_base(const FaParams &p, long long head_off,
+                                                           int row0, int page) {
+        if (page < 0 || page >= p.num_blocks) page = 0;
+        return static_cast<long long>(page) * p.page_stride + head_off +
+               static_cast<long long>(row0 & (p.bs - 1)) * D;
+    }
+
+    __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
+                                         int j0, int kv_limit) {
+        const int lane = min(static_cast<int>(threadIdx.x & 63), 47);
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int kr = lane / 12, kc = lane % 12;          // K: row in group of 4, chunk
+        const int vr = 2 * (lane & 3), vc = lane >> 2;     // V: row pair, column block
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int row0 = j0 + w * RW + 4 * i;
+            k[i] = load16<STREAM>(p.kc + group_base(p, head_off, row0, pg[i]) + kr * D + kc * 8);
+        }
+        vok = 0;
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int row0 = j0 + w * RW + 8 * i;
+            const uint16_t *src = p.vc + group_base(p, head_off, row0, pg[KI + i]) + vr * D + vc * 8;
+            v[i][0] = load16<STREAM>(src);
+            v[i][1] = load16<STREAM>(src + D);
+            vok |= (row0 + vr < kv_limit ? 1u : 0u) << (2 * i);
+            vok |= (row0 + vr + 1 < kv_limit ? 1u : 0u) << (2 * i + 1);
+        }
+        prefetch(p, bt_row, j0 + TILE, kv_limit);
+    }
+
+    __device__ __forceinline__ void store(uint16_t *buf) const {
+        const int lane = threadIdx.x & 63;
+        if (lane >= 48) return;
+        uint16_t *Ks = buf;
+        uint16_t *Vt = buf + TILE * KP;
+        const int w = threadIdx.x >> 6;
+        const int kr = lane / 12, kc = lane % 12;
+        const int vr = 2 * (lane & 3), vc = lane >> 2;
+#pragma unroll
+        for (int i = 0; i < KI; ++i)
+            *reinterpret_cast<u32x4 *>(Ks + (w * RW + 4 * i + kr) * KP + kc * 8) = k[i];
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int r = w * RW + 8 * i + vr;
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            const u32x4 a = (vok >> (2 * i)) & 1u ? v[i][0] : zero;
+            const u32x4 b = (vok >> (2 * i + 1)) & 1u ? v[i][1] : zero;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = __builtin_amdgcn_perm(b[e], a[e], 0x05040100u);
+                const uint32_t hi = __builtin_amdgcn_perm(b[e], a[e], 0x07060302u);
+                *reinterpret_cast<uint32_t *>(Vt + (8 * vc + 2 * e) * VP + r) = lo;
+                *reinterpret_cast<uint32_t *>(Vt + (8 * vc + 2 * e + 1) * VP + r) = hi;
+            }
+        }
+    }
+};
+
 // Loader choice: the uniform-page loader when it applies, else TileLoader.
 // STREAM marks K/V read once per launch (decode): non-temporal loads.
 template <int D, int TILE, int W, bool POW2, bool STREAM = false>
@@ -485,6 +576,10 @@ struct LoaderSel<128, TILE, W, true, STREAM> {
 template <int TILE, int W, bool STREAM>
 struct LoaderSel<64, TILE, W, true, STREAM> {
     using type = PagedLoader64<TILE, W, STREAM>;
+};
+template <int TILE, int W, bool STREAM>
+struct LoaderSel<96, TILE, W, true, STREAM> {
+    using type = PagedLoader96<TILE, W, STREAM>;
 };
 
 template <typename T> struct Ones2;

@@ -383,16 +383,17 @@ def test_head_sizes(D, dt):
 
 
 @pytest.mark.parametrize("bs", [8, 16, 32, 5])
-def test_head_size_64_block_sizes(bs):
-    """D = 64 with block sizes 8 (the page-uniform loader's V groups of 16
-    rows then span two cache blocks), 16, 32 and 5 (the generic loader):
-    prefill with a cached prefix, decode and a chunk."""
+@pytest.mark.parametrize("D", [64, 96])
+def test_head_size_64_96_block_sizes(D, bs):
+    """D = 64 and 96 with block sizes 8 (for D = 64 the page-uniform loader's
+    V groups of 16 rows then span two cache blocks), 16, 32 and 5 (the
+    generic loader): prefill with a cached prefix, decode and a chunk."""
     for name, H, Hkv, q_lens, kv_lens in (("prefill", 8, 2, [130, 77], [300, 77]),
                                           ("decode", 16, 4, [1, 1, 1], [3, 700, 2500]),
                                           ("chunk", 8, 4, [33, 20], [90, 20])):
-        case = dict(name=f"D=64 bs={bs} {name}", H=H, Hkv=Hkv, D=64, bs=bs, q_lens=q_lens,
+        case = dict(name=f"D={D} bs={bs} {name}", H=H, Hkv=Hkv, D=D, bs=bs, q_lens=q_lens,
                     kv_lens=kv_lens)
-        check(case, orc.BF16, seed=bs + len(name))
+        check(case, orc.BF16, seed=bs + D + len(name))
 
 
 # ------------------------------------------------------------------------
