@@ -1147,6 +1147,18 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) fa_decode_kernel(FaParam
     const int kv_lo = split * p.split_len;
     const int kv_hi = split == decode_items(p, L, S) - 1 ? S : min(S, kv_lo + p.split_len);
     decode_pass<T, D, POW2>(p, smem, b, kvh, q_off, L, S, kv_lo, kv_hi, p.rq, 0);
+    if (p.max_splits == 1) {
+        // one split per sequence: the rows are final here, normalised with
+        // the merge kernel's arithmetic (the reciprocal of l, then a product),
+        // and no merge kernel runs
+        merge_waves<D>(smem, p.ncols, [&](int c, int d, float acc, float, float l) {
+            const int hl = c / p.rq, row = c % p.rq;
+            if (hl >= p.G || row >= L) return;
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            p.o[((q_off + row) * p.H + kvh * p.G + hl) * D + d] = Cvt<T>::from(inv * acc);
+        });
+        return;
+    }
     const long long base = ((static_cast<long long>(b) * p.Hkv + kvh) * p.max_splits + split) *
                            p.ncols;
     merge_waves<D>(smem, p.ncols, [&](int c, int d, float acc, float M, float l) {
@@ -1320,9 +1332,11 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
         dim3 grid(p.batch * p.Hkv, pl.max_splits);
         hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, p);
         TECO_CHECK_LAUNCH("flash_attention decode");
-        hipLaunchKernelGGL((fa_decode_combine_kernel<T, D>), dim3(p.batch * p.Hkv), dim3(256), 0,
-                           s, p);
-        TECO_CHECK_LAUNCH("flash_attention combine");
+        if (pl.max_splits > 1) {
+            hipLaunchKernelGGL((fa_decode_combine_kernel<T, D>), dim3(p.batch * p.Hkv), dim3(256),
+                               0, s, p);
+            TECO_CHECK_LAUNCH("flash_attention combine");
+        }
         return TECOOPS_STATUS_SUCCESS;
     }
     if constexpr (D == 128) {

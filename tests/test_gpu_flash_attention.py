@@ -330,6 +330,23 @@ def test_decode_work_order_large_batch(entry):
     assert_close(got, ref, what=f"decode order, 150 sequences ({entry})")
 
 
+@pytest.mark.parametrize("dt", [orc.HALF, orc.BF16], ids=["fp16", "bf16"])
+def test_decode_single_split(dt):
+    """Every kv length within one split (<= 512 keys): the decode workgroups
+    write the output rows themselves and no merge kernel runs; with empty
+    sequences and a row range past the decode bound."""
+    r = np.random.default_rng(88)
+    kv = r.integers(1, 450, 90).tolist()
+    kv[7] = 0
+    q_lens = [1] * 90
+    q_lens[11] = 5  # 4 * 5 > 32 columns: the multi-pass path
+    kv[11] = 300
+    q, kc, vc, bt = make_inputs(89, 16, 4, 128, 16, q_lens, kv, dtype=dt)
+    got = run_gpu(q, kc, vc, bt, q_lens, kv, dt, max_q=1)
+    ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=dt)
+    assert_close(got, ref, what="decode, one split per sequence")
+
+
 def test_prefill_rows_past_max_seqlen_q():
     """Prefill grid sized from an understated max_seqlen_q: workgroups take the
     query tiles past the grid in turn."""
