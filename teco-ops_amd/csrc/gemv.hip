@@ -471,7 +471,8 @@ gemv_i8_mfma_kernel(const int8_t *__restrict__ W, const uint16_t *__restrict__ s
 // values.  The 16 blocks hold partial sums over disjoint k; once the wave has
 // covered K they are added across lanes l, l + 4, ..., l + 60 without LDS
 // (DPP row rotations by 4 and 8, then the row-pair and half-wave permlane
-// swaps).  No cross-wave reduction or barrier follows the staging of x.
+// swaps).  Unless K is split over two waves (small N), no cross-wave
+// reduction or barrier follows the staging of x.
 //   x is staged in LDS as [4*NCG][K] 16-bit values with the 16-byte chunks of
 //   row i XOR-swizzled by 4*(i % 4) inside each 256-byte run, so that the
 //   128-bit B-operand reads of lanes 0-7 (rows 0-3, two chunks) hit distinct
@@ -510,7 +511,9 @@ __device__ __forceinline__ int xs_chunk(int row, int c, int K) {
 // T: element type of x / y (and W unless I8).  NCG: batch column groups of 4
 // (1 for B <= 4, else 2).  RG: groups of 4 rows per wave, which share each x
 // read from LDS.  CPL: load steps a lane keeps in flight (RG loads each).
-template <typename T, bool I8, int NCG, int RG, int NW, int CPL>
+// KS: waves per row group, each sweeping 1/KS of K; their sums meet in LDS
+// (KS = 2 when N is small, so that the grid still has enough waves).
+template <typename T, bool I8, int NCG, int RG, int NW, int CPL, int KS>
 __global__ void __launch_bounds__(NW * 64)
 gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
                const uint4 *__restrict__ x, uint16_t *__restrict__ y, int N, int K, int B) {
@@ -518,10 +521,12 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
     uint16_t *xs = reinterpret_cast<uint16_t *>(xs_raw);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int GW = NW / KS;          // row groups per workgroup
+    const int gw = wave % GW, part = wave / GW;
     const int r = lane & 3, blk = lane >> 2;
-    const int n0 = (blockIdx.x * NW + wave) * 4 * RG;
+    const int n0 = (blockIdx.x * GW + gw) * 4 * RG;
     const int kw = I8 ? K / 16 : K / 8;  // 16-byte chunks of a W row
-    const int nl = kw / 16;              // load steps per row
+    const int nl = kw / 16 / KS;         // load steps per row and part
     const uint4 *wr[RG];
 #pragma unroll
     for (int g = 0; g < RG; ++g)
@@ -573,8 +578,8 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
     // Each wave starts its sweep of K at a different load step, so that the
     // requests in flight across the grid spread over all HBM channels instead
     // of every wave reading the same offset of its rows at the same time.
-    const int rot = (blockIdx.x * NW + wave) % nl;
-    const auto step = [&](int i) { return i + rot < nl ? i + rot : i + rot - nl; };
+    const int rot = (blockIdx.x * GW + gw) % nl;
+    const auto step = [&](int i) { return part * nl + (i + rot < nl ? i + rot : i + rot - nl); };
     // Waves past the last row still stage x and reach the barrier; their
     // loads read row N - 1 and their sums are never stored.
     ring_steps<CPL>(
@@ -644,6 +649,30 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
             }
             __syncthreads();
         });
+    if constexpr (KS == 2) {
+        // part 1 hands its sums to part 0 through LDS past the staged x:
+        // value e of lane l of row group gw at red[e][gw * 64 + l], so that
+        // the 64 lanes of a wave touch 64 consecutive words per value
+        float *mine = reinterpret_cast<float *>(xs + 4 * NCG * K) + gw * 64 + lane;
+        if (part == 1) {
+#pragma unroll
+            for (int g = 0; g < RG; ++g)
+#pragma unroll
+                for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        mine[((g * NCG + cg) * 4 + v) * GW * 64] = acc[g][cg][v];
+        }
+        __syncthreads();
+        if (part == 1) return;
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    acc[g][cg][v] += mine[((g * NCG + cg) * 4 + v) * GW * 64];
+    }
     if (n0 >= N) return;
     // add the 16 blocks' partial sums (lanes r, r + 4, ..., r + 60: rotations
     // by 4 and 8 within each row of 16 lanes, then the row-pair and half-wave
@@ -739,6 +768,12 @@ constexpr int kB8RgF16 = 1, kB8CplF16 = 8, kB8RgI8 = 1, kB8CplI8 = 2;
 // N = 6144, K = 4096 at batch 4: 9.0 against 7.2 us.  At N = 14336 and 28672,
 // batch 8, 8 in flight was slower (12.7 -> 16.3 and 23.6 -> 30.3 us).
 constexpr int kB8SmallN = 8192, kB8CplI8Small = 8;
+// Below kB8SplitN rows two waves share each row group, each sweeping half of
+// K, so that the grid holds twice the waves: N = 4096, K = 14336 at batch 4 /
+// 8: fp16 27.5 / 54.7 -> 22.1 / 44.0 us, int8 16.9 / 34.2 -> 13.7 / 27.0 us;
+// N = 4096, K = 4096, batch 8: fp16 11.0 -> 9.5 us.  Loads in flight per
+// lane: 8 fp16 / 4 int8 (4 / 8 and 16 / 2 were slower at most shapes).
+constexpr int kB8SplitN = 8192, kB8CplF16Split = 8, kB8CplI8Split = 4;
 constexpr int kB8MaxBatch = 8;
 
 // Rows of x the 4x4x4 path takes per launch for this batch and K (0: the
@@ -762,12 +797,15 @@ int vec_slice(int batch, int k) {
 // leaves the busiest CU the fewest waves (ceil(workgroups / CUs) * waves; the
 // first listed on ties), so that a grid just short of the CU count does not
 // idle CUs: N = 14336 takes 14 waves and 256 workgroups (16 waves: 224).
-int b8_waves(int N, int rows_per_wave) {
+// With K split over ks waves a workgroup covers nw / ks row groups (nw even).
+int b8_waves(int N, int rows_per_wave, int ks) {
     const long long cus = tecoops::device_cus();
     int best = 16;
     long long best_load = -1;
     for (int nw : {16, 14, 12, 8, 7}) {
-        const long long wgs = tecoops::ceil_div(N, static_cast<long long>(rows_per_wave) * nw);
+        if (nw % ks != 0) continue;
+        const long long wgs =
+            tecoops::ceil_div(N, static_cast<long long>(rows_per_wave) * (nw / ks));
         const long long load = (wgs + cus - 1) / cus * nw;
         if (best_load < 0 || load < best_load) {
             best_load = load;
@@ -777,37 +815,53 @@ int b8_waves(int N, int rows_per_wave) {
     return best;
 }
 
-template <typename T, bool I8, int NCG, int NW, int CPL>
+// LDS bytes of the 4x4x4 path: staged x, plus the partial sums handed
+// between the K halves when ks = 2.
+size_t b8_lds(int ncg, int rg, int nw, int ks, int K) {
+    return 4 * ncg * static_cast<size_t>(K) * 2 +
+           (ks == 2 ? static_cast<size_t>(rg) * ncg * 4 * (nw / 2) * 64 * 4 : 0);
+}
+
+template <typename T, bool I8, int NCG, int NW, int CPL, int KS>
 bool launch_b8_nw(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                   hipStream_t s) {
     constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
-    const size_t lds = 4 * NCG * static_cast<size_t>(K) * 2;
-    auto *kern = &gemv_b8_kernel<T, I8, NCG, RG, NW, CPL>;
+    const size_t lds = b8_lds(NCG, RG, NW, KS, K);
+    auto *kern = &gemv_b8_kernel<T, I8, NCG, RG, NW, CPL, KS>;
     if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds)) return false;
-    hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(N, 4 * RG * NW)), dim3(NW * 64), lds, s,
+    hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(N, 4 * RG * (NW / KS))), dim3(NW * 64), lds, s,
                        static_cast<const uint4 *>(W), static_cast<const uint16_t *>(sc),
                        static_cast<const uint4 *>(x), static_cast<uint16_t *>(y), N, K, B);
     return true;
 }
 
-template <typename T, bool I8, int NCG, int CPL>
+template <typename T, bool I8, int NCG, int CPL, int KS>
 bool launch_b8_cpl(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                    hipStream_t s) {
-    switch (b8_waves(N, 4 * (I8 ? kB8RgI8 : kB8RgF16))) {
-        case 14: return launch_b8_nw<T, I8, NCG, 14, CPL>(W, sc, x, y, B, N, K, s);
-        case 12: return launch_b8_nw<T, I8, NCG, 12, CPL>(W, sc, x, y, B, N, K, s);
-        case 8: return launch_b8_nw<T, I8, NCG, 8, CPL>(W, sc, x, y, B, N, K, s);
-        case 7: return launch_b8_nw<T, I8, NCG, 7, CPL>(W, sc, x, y, B, N, K, s);
-        default: return launch_b8_nw<T, I8, NCG, 16, CPL>(W, sc, x, y, B, N, K, s);
+    switch (b8_waves(N, 4 * (I8 ? kB8RgI8 : kB8RgF16), KS)) {
+        case 14: return launch_b8_nw<T, I8, NCG, 14, CPL, KS>(W, sc, x, y, B, N, K, s);
+        case 12: return launch_b8_nw<T, I8, NCG, 12, CPL, KS>(W, sc, x, y, B, N, K, s);
+        case 8: return launch_b8_nw<T, I8, NCG, 8, CPL, KS>(W, sc, x, y, B, N, K, s);
+        case 7:
+            if constexpr (KS == 1) return launch_b8_nw<T, I8, NCG, 7, CPL, KS>(W, sc, x, y, B, N, K, s);
+            return false;
+        default: return launch_b8_nw<T, I8, NCG, 16, CPL, KS>(W, sc, x, y, B, N, K, s);
     }
 }
 
 template <typename T, bool I8, int NCG>
 bool launch_b8_ncg(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                    hipStream_t s) {
+    constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
+    // K split over two waves: each half a whole number of load steps (16
+    // chunks of 16 bytes per row), and the sums' LDS beside x
+    if (N < kB8SplitN && K % (I8 ? 512 : 256) == 0 &&
+        b8_lds(NCG, RG, 16, 2, K) <= static_cast<size_t>(kMaxLdsBytes))
+        return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8Split : kB8CplF16Split, 2>(W, sc, x, y, B,
+                                                                                   N, K, s);
     if (I8 && N < kB8SmallN)
-        return launch_b8_cpl<T, I8, NCG, kB8CplI8Small>(W, sc, x, y, B, N, K, s);
-    return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8 : kB8CplF16>(W, sc, x, y, B, N, K, s);
+        return launch_b8_cpl<T, I8, NCG, kB8CplI8Small, 1>(W, sc, x, y, B, N, K, s);
+    return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8 : kB8CplF16, 1>(W, sc, x, y, B, N, K, s);
 }
 
 template <typename T, bool I8>

@@ -731,6 +731,36 @@ def test_gemv_int8_small_batch_matrix_core(B, K):
                  what=f"gemv_int8 {B}x{N}x{K}")
 
 
+@pytest.mark.parametrize("B,N,K", [(3, 301, 256), (8, 4099, 2304), (5, 8191, 4096),
+                                   (2, 1000, 14336), (4, 6144, 512)])
+@pytest.mark.parametrize("i8", [False, True], ids=["fp16", "int8"])
+def test_gemv_split_k(B, N, K, i8):
+    """Below 8192 rows the 4x4x4 path gives each row group two waves, each
+    sweeping half of K, and adds their sums through LDS: halves of 1 load
+    step (K = 256 fp16 / 512 int8), 9 and 5 steps (not multiples of the
+    ring depth), a partial row group and waves past the last row; an int8 K
+    that is an odd number of 256-k steps (2304) takes the unsplit kernel."""
+    if B == 2 and not i8:
+        B = 3  # fp16 batch 2 runs the VALU path
+    r = rng(960 + N + K + B + i8)
+    x = bits(r.standard_normal((B, K)))
+    y = torch.empty((B, N), dtype=torch.float16, device="cuda")
+    if i8:
+        W = r.integers(-127, 128, (N, K), dtype=np.int8)
+        s = bits(r.uniform(0.001, 0.01, N))
+        ref = orc.gemv_int8(W, s, x)
+        tecoops.gemv_int8(dev(W), dev(s), dev(x), y)
+        torch.cuda.synchronize()
+        assert_close(as_f32(y), ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2,
+                     what=f"gemv_int8 {B}x{N}x{K}")
+    else:
+        W = bits(r.normal(0, 0.05, (N, K)))
+        ref = orc.gemv(W, x)
+        tecoops.gemv(dev(W), dev(x), y)
+        torch.cuda.synchronize()
+        assert_close(as_f32(y), ref, what=f"gemv {B}x{N}x{K}")
+
+
 @pytest.mark.parametrize("N", [16384, 14336, 12288, 301])
 @pytest.mark.parametrize("i8", [False, True])
 def test_gemv_small_batch_workgroup_sizes(N, i8):
