@@ -513,10 +513,13 @@ __device__ __forceinline__ int xs_chunk(int row, int c, int K) {
 // read from LDS.  CPL: load steps a lane keeps in flight (RG loads each).
 // KS: waves per row group, each sweeping 1/KS of K; their sums meet in LDS
 // (KS = 2 when N is small, so that the grid still has enough waves).
-template <typename T, bool I8, int NCG, int RG, int NW, int CPL, int KS>
+// PHASED: K is swept in nph equal phases, x staged in LDS one phase at a
+// time (rows whose whole x does not fit in LDS); W is still read once.
+template <typename T, bool I8, int NCG, int RG, int NW, int CPL, int KS, bool PHASED>
 __global__ void __launch_bounds__(NW * 64)
 gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
-               const uint4 *__restrict__ x, uint16_t *__restrict__ y, int N, int K, int B) {
+               const uint4 *__restrict__ x, uint16_t *__restrict__ y, int N, int K, int B,
+               int nph_arg) {
     extern __shared__ uint4 xs_raw[];
     uint16_t *xs = reinterpret_cast<uint16_t *>(xs_raw);
     const int lane = threadIdx.x & 63;
@@ -525,13 +528,16 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
     const int gw = wave % GW, part = wave / GW;
     const int r = lane & 3, blk = lane >> 2;
     const int n0 = (blockIdx.x * GW + gw) * 4 * RG;
+    const int nph = PHASED ? nph_arg : 1;
+    const int kp = K / nph;              // k values per phase
     const int kw = I8 ? K / 16 : K / 8;  // 16-byte chunks of a W row
-    const int nl = kw / 16 / KS;         // load steps per row and part
+    const int nl = kw / nph / 16 / KS;   // load steps per row, part and phase
     const uint4 *wr[RG];
 #pragma unroll
     for (int g = 0; g < RG; ++g)
         wr[g] = W + static_cast<long long>(min(n0 + 4 * g + r, N - 1)) * kw + blk;
-    const int kx = K / 8;  // 16-byte chunks of an x row
+    const int kx = K / 8;    // 16-byte chunks of an x row
+    const int kxp = kp / 8;  // ... of one phase
     f32x4_t acc[RG][NCG];
 #pragma unroll
     for (int g = 0; g < RG; ++g)
@@ -548,112 +554,123 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
             for (int v = 0; v < 4; ++v) sc[g][v] = scales[min(n0 + 4 * g + v, N - 1)];
     }
     constexpr int XPT = (kMaxXChunks + NW * 64 - 1) / (NW * 64);  // x chunks per thread
-    const int nxc = NCG * 4 * kx;
-    uint4 xr[XPT];
-#pragma unroll
-    for (int j = 0; j < XPT; ++j) {
-        const int idx = min(static_cast<int>(threadIdx.x) + j * NW * 64, nxc - 1);
-        const int row = min(idx / kx, B - 1);
-        xr[j] = x[static_cast<long long>(row) * kx + idx % kx];
-    }
-    // int8 W on a full-GPU grid: every CU's x loads miss L2 together and, at
-    // HBM, queue behind the first W loads of all waves, which start at the
-    // same moment, while no wave can use its W before x is in LDS.  Pausing
-    // ~1000 cycles before the W loads lets the x misses reach HBM first
-    // (batch 8 x [14336, 4096], A/B on two boxes: 13.4 -> 12.9 us and
-    // 14.0 -> 13.8 us; waiting for x outright: 14.0 us; fp16 W, twice the
-    // bytes per x byte, gains nothing).  With 2 W steps in flight per lane,
-    // pauses of 0, 8, 16 and 32 (x 64 cycles) took 13.5-14.0, 13.4, 12.9-13.1
-    // and 13.3 us on one box.
-    if constexpr (I8) {
-        if (gridDim.x >= 128) __builtin_amdgcn_s_sleep(16);
-    }
+    const int nxc = NCG * 4 * kxp;
     // This lane's x chunks in LDS: chunk 16i + blk (fp16 W) or 32i + 2blk and
     // the next (int8 W) of row 4cg + r.  The swizzle xor (4r < 16) stays below
-    // the step's bits, so xs_chunk(4cg + r, c0 + 16i, K) = xs_chunk(4cg + r,
-    // c0, K) + 128i (c0 = blk), likewise with 32i (c0 = 2blk), and rows 4
+    // the step's bits, so xs_chunk(4cg + r, c0 + 16i, kp) = xs_chunk(4cg + r,
+    // c0, kp) + 128i (c0 = blk), likewise with 32i (c0 = 2blk), and rows 4
     // apart keep the same xor: one base address per lane.
-    const uint16_t *xs_lane = xs + xs_chunk(r, I8 ? 2 * blk : blk, K);
+    const uint16_t *xs_lane = xs + xs_chunk(r, I8 ? 2 * blk : blk, kp);
     uint4 q[CPL][RG];
     // Each wave starts its sweep of K at a different load step, so that the
     // requests in flight across the grid spread over all HBM channels instead
     // of every wave reading the same offset of its rows at the same time.
     const int rot = (blockIdx.x * GW + gw) % nl;
-    const auto step = [&](int i) { return part * nl + (i + rot < nl ? i + rot : i + rot - nl); };
-    // Waves past the last row still stage x and reach the barrier; their
-    // loads read row N - 1 and their sums are never stored.
-    ring_steps<CPL>(
-        nl,
-        [&](int i, int u) {
-            const int st = 16 * step(i);
+    const auto local = [&](int i) { return part * nl + (i + rot < nl ? i + rot : i + rot - nl); };
+    for (int ph = 0; ph < nph; ++ph) {
+        const int xc0 = ph * kxp;       // the phase's first chunk of an x row
+        const int st0 = ph * nl * KS;   // ... and first load step of a W row
+        uint4 xr[XPT];
 #pragma unroll
-            for (int g = 0; g < RG; ++g) q[u][g] = load_stream(wr[g] + st);
-        },
-        [&](int i0, int u) {
-            const int i = step(i0);
-            if constexpr (I8) {
-                uint32_t p[RG][8];
+        for (int j = 0; j < XPT; ++j) {
+            const int idx = min(static_cast<int>(threadIdx.x) + j * NW * 64, nxc - 1);
+            const int row = min(idx / kxp, B - 1);
+            xr[j] = x[static_cast<long long>(row) * kx + xc0 + idx % kxp];
+        }
+        // int8 W on a full-GPU grid: every CU's x loads miss L2 together and,
+        // at HBM, queue behind the first W loads of all waves, which start at
+        // the same moment, while no wave can use its W before x is in LDS.
+        // Pausing ~1000 cycles before the W loads lets the x misses reach HBM
+        // first (batch 8 x [14336, 4096], A/B on two boxes: 13.4 -> 12.9 us
+        // and 14.0 -> 13.8 us; waiting for x outright: 14.0 us; fp16 W, twice
+        // the bytes per x byte, gains nothing).  With 2 W steps in flight per
+        // lane, pauses of 0, 8, 16 and 32 (x 64 cycles) took 13.5-14.0, 13.4,
+        // 12.9-13.1 and 13.3 us on one box.
+        if constexpr (I8) {
+            if (ph == 0 && gridDim.x >= 128) __builtin_amdgcn_s_sleep(16);
+        }
+        // Waves past the last row still stage x and reach the barriers; their
+        // loads read row N - 1 and their sums are never stored.
+        ring_steps<CPL>(
+            nl,
+            [&](int i, int u) {
+                const int st = 16 * (st0 + local(i));
 #pragma unroll
-                for (int g = 0; g < RG; ++g) {
-                    widen_i8(q[u][g].x, p[g][0], p[g][1]);
-                    widen_i8(q[u][g].y, p[g][2], p[g][3]);
-                    widen_i8(q[u][g].z, p[g][4], p[g][5]);
-                    widen_i8(q[u][g].w, p[g][6], p[g][7]);
-                }
-#pragma unroll
-                for (int cg = 0; cg < NCG; ++cg) {
-                    // chunks 32i + 2blk and 32i + 2blk + 1 of row 4cg + r
-                    const uint4 *xp = reinterpret_cast<const uint4 *>(xs_lane + cg * 4 * K) + 32 * i;
-                    const uint4 xa = xp[0];
-                    const uint4 xb = xp[1];
-#pragma unroll
-                    for (int g = 0; g < RG; ++g) {
-                        f32x4_t c = acc[g][cg];
-                        c = Mma4<f16>::run(p[g][0], p[g][1], xa.x, xa.y, c);
-                        c = Mma4<f16>::run(p[g][2], p[g][3], xa.z, xa.w, c);
-                        c = Mma4<f16>::run(p[g][4], p[g][5], xb.x, xb.y, c);
-                        c = Mma4<f16>::run(p[g][6], p[g][7], xb.z, xb.w, c);
-                        acc[g][cg] = c;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int cg = 0; cg < NCG; ++cg) {
-                    // chunk 16i + blk of row 4cg + r
-                    const uint4 xv = reinterpret_cast<const uint4 *>(xs_lane + cg * 4 * K)[16 * i];
+                for (int g = 0; g < RG; ++g) q[u][g] = load_stream(wr[g] + st);
+            },
+            [&](int i0, int u) {
+                const int i = local(i0);
+                if constexpr (I8) {
+                    uint32_t p[RG][8];
 #pragma unroll
                     for (int g = 0; g < RG; ++g) {
-                        acc[g][cg] = Mma4<T>::run(q[u][g].x, q[u][g].y, xv.x, xv.y, acc[g][cg]);
-                        acc[g][cg] = Mma4<T>::run(q[u][g].z, q[u][g].w, xv.z, xv.w, acc[g][cg]);
+                        widen_i8(q[u][g].x, p[g][0], p[g][1]);
+                        widen_i8(q[u][g].y, p[g][2], p[g][3]);
+                        widen_i8(q[u][g].z, p[g][4], p[g][5]);
+                        widen_i8(q[u][g].w, p[g][6], p[g][7]);
+                    }
+#pragma unroll
+                    for (int cg = 0; cg < NCG; ++cg) {
+                        // chunks 32i + 2blk and 32i + 2blk + 1 of row 4cg + r
+                        const uint4 *xp =
+                            reinterpret_cast<const uint4 *>(xs_lane + cg * 4 * kp) + 32 * i;
+                        const uint4 xa = xp[0];
+                        const uint4 xb = xp[1];
+#pragma unroll
+                        for (int g = 0; g < RG; ++g) {
+                            f32x4_t c = acc[g][cg];
+                            c = Mma4<f16>::run(p[g][0], p[g][1], xa.x, xa.y, c);
+                            c = Mma4<f16>::run(p[g][2], p[g][3], xa.z, xa.w, c);
+                            c = Mma4<f16>::run(p[g][4], p[g][5], xb.x, xb.y, c);
+                            c = Mma4<f16>::run(p[g][6], p[g][7], xb.z, xb.w, c);
+                            acc[g][cg] = c;
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int cg = 0; cg < NCG; ++cg) {
+                        // chunk 16i + blk of row 4cg + r
+                        const uint4 xv =
+                            reinterpret_cast<const uint4 *>(xs_lane + cg * 4 * kp)[16 * i];
+#pragma unroll
+                        for (int g = 0; g < RG; ++g) {
+                            acc[g][cg] =
+                                Mma4<T>::run(q[u][g].x, q[u][g].y, xv.x, xv.y, acc[g][cg]);
+                            acc[g][cg] =
+                                Mma4<T>::run(q[u][g].z, q[u][g].w, xv.z, xv.w, acc[g][cg]);
+                        }
                     }
                 }
-            }
-        },
-        // the x chunks reach LDS once the first W loads are in flight; an x
-        // larger than the register-staged part (K > 4096 for 8 rows of x)
-        // copies the rest directly
-        [&] {
+            },
+            // the phase's x chunks reach LDS once its first W loads are in
+            // flight (after every wave has finished the previous phase); an
+            // x larger than the register-staged part (more than 4096 chunks)
+            // copies the rest directly
+            [&] {
+                if (ph > 0) __syncthreads();
 #pragma unroll
-            for (int j = 0; j < XPT; ++j) {
-                const int idx = threadIdx.x + j * NW * 64;
-                if (idx < nxc) {
-                    const int row = idx / kx, c = idx - row * kx;
-                    *reinterpret_cast<uint4 *>(xs + xs_chunk(row, c, K)) =
-                        row < B ? xr[j] : uint4{0u, 0u, 0u, 0u};
+                for (int j = 0; j < XPT; ++j) {
+                    const int idx = threadIdx.x + j * NW * 64;
+                    if (idx < nxc) {
+                        const int row = idx / kxp, c = idx - row * kxp;
+                        *reinterpret_cast<uint4 *>(xs + xs_chunk(row, c, kp)) =
+                            row < B ? xr[j] : uint4{0u, 0u, 0u, 0u};
+                    }
                 }
-            }
-            for (int idx = threadIdx.x + XPT * NW * 64; idx < nxc; idx += NW * 64) {
-                const int row = idx / kx, c = idx - row * kx;
-                *reinterpret_cast<uint4 *>(xs + xs_chunk(row, c, K)) =
-                    row < B ? x[static_cast<long long>(row) * kx + c] : uint4{0u, 0u, 0u, 0u};
-            }
-            __syncthreads();
-        });
+                for (int idx = threadIdx.x + XPT * NW * 64; idx < nxc; idx += NW * 64) {
+                    const int row = idx / kxp, c = idx - row * kxp;
+                    *reinterpret_cast<uint4 *>(xs + xs_chunk(row, c, kp)) =
+                        row < B ? x[static_cast<long long>(row) * kx + xc0 + c]
+                                : uint4{0u, 0u, 0u, 0u};
+                }
+                __syncthreads();
+            });
+    }
     if constexpr (KS == 2) {
         // part 1 hands its sums to part 0 through LDS past the staged x:
         // value e of lane l of row group gw at red[e][gw * 64 + l], so that
         // the 64 lanes of a wave touch 64 consecutive words per value
-        float *mine = reinterpret_cast<float *>(xs + 4 * NCG * K) + gw * 64 + lane;
+        float *mine = reinterpret_cast<float *>(xs + 4 * NCG * kp) + gw * 64 + lane;
         if (part == 1) {
 #pragma unroll
             for (int g = 0; g < RG; ++g)
@@ -776,15 +793,6 @@ constexpr int kB8SmallN = 8192, kB8CplI8Small = 8;
 constexpr int kB8SplitN = 8192, kB8CplF16Split = 8, kB8CplI8Split = 4;
 constexpr int kB8MaxBatch = 8;
 
-// Rows of x the 4x4x4 path takes per launch for this batch and K (0: the
-// path does not apply): the whole batch when its staged x (4 or 8 rows) fits
-// in LDS, else slices of 4 rows, each launch streaming W once.
-int b8_slice(int batch, int k, bool i8) {
-    if (batch > kB8MaxBatch || k % (i8 ? 256 : 128) != 0) return 0;
-    if (static_cast<long long>(batch <= 4 ? 4 : 8) * k * 2 <= kMaxLdsBytes) return batch;
-    return 4LL * k * 2 <= kMaxLdsBytes ? 4 : 0;
-}
-
 // Rows of x per launch of the VALU path (x [rows, K] staged in LDS): up to 8.
 int vec_slice(int batch, int k) {
     long long rows = kMaxLdsBytes / (2LL * k);
@@ -815,37 +823,69 @@ int b8_waves(int N, int rows_per_wave, int ks) {
     return best;
 }
 
-// LDS bytes of the 4x4x4 path: staged x, plus the partial sums handed
-// between the K halves when ks = 2.
-size_t b8_lds(int ncg, int rg, int nw, int ks, int K) {
-    return 4 * ncg * static_cast<size_t>(K) * 2 +
+// LDS bytes of the 4x4x4 path: staged x (kp values of 4 * ncg rows), plus
+// the partial sums handed between the K halves when ks = 2.
+size_t b8_lds(int ncg, int rg, int nw, int ks, int kp) {
+    return 4 * ncg * static_cast<size_t>(kp) * 2 +
            (ks == 2 ? static_cast<size_t>(rg) * ncg * 4 * (nw / 2) * 64 * 4 : 0);
+}
+
+// Phases the 4x4x4 path sweeps K in (x staged one phase at a time): the
+// fewest equal phases, each a whole number of load steps for each of the ks
+// waves of a row group, whose LDS fits; 0 if none up to kB8MaxPhases does.
+constexpr int kB8MaxPhases = 8;
+int b8_phases(int ncg, int rg, int ks, int k, bool i8) {
+    const int step = (i8 ? 256 : 128) * ks;  // k values per load step of all ks waves
+    for (int nph = 1; nph <= kB8MaxPhases; ++nph)
+        if (k % (nph * step) == 0 &&
+            b8_lds(ncg, rg, 16, ks, k / nph) <= static_cast<size_t>(kMaxLdsBytes))
+            return nph;
+    return 0;
+}
+
+// Rows of x the 4x4x4 path takes per launch for this batch and K (0: the
+// path does not apply): the whole batch when its staged x (4 or 8 rows) fits
+// in LDS in at most kB8MaxPhases phases, else slices of 4 rows, each launch
+// streaming W once.
+int b8_slice(int batch, int k, bool i8) {
+    if (batch > kB8MaxBatch) return 0;
+    const int rg = i8 ? kB8RgI8 : kB8RgF16;
+    if (b8_phases(batch <= 4 ? 1 : 2, rg, 1, k, i8) > 0) return batch;
+    return b8_phases(1, rg, 1, k, i8) > 0 ? 4 : 0;
+}
+
+template <typename T, bool I8, int NCG, int NW, int CPL, int KS, bool PHASED>
+bool launch_b8_ph(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
+                  int nph, hipStream_t s) {
+    constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
+    const size_t lds = b8_lds(NCG, RG, NW, KS, K / nph);
+    auto *kern = &gemv_b8_kernel<T, I8, NCG, RG, NW, CPL, KS, PHASED>;
+    if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds)) return false;
+    hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(N, 4 * RG * (NW / KS))), dim3(NW * 64), lds, s,
+                       static_cast<const uint4 *>(W), static_cast<const uint16_t *>(sc),
+                       static_cast<const uint4 *>(x), static_cast<uint16_t *>(y), N, K, B, nph);
+    return true;
 }
 
 template <typename T, bool I8, int NCG, int NW, int CPL, int KS>
 bool launch_b8_nw(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
-                  hipStream_t s) {
-    constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
-    const size_t lds = b8_lds(NCG, RG, NW, KS, K);
-    auto *kern = &gemv_b8_kernel<T, I8, NCG, RG, NW, CPL, KS>;
-    if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds)) return false;
-    hipLaunchKernelGGL(kern, dim3(tecoops::ceil_div(N, 4 * RG * (NW / KS))), dim3(NW * 64), lds, s,
-                       static_cast<const uint4 *>(W), static_cast<const uint16_t *>(sc),
-                       static_cast<const uint4 *>(x), static_cast<uint16_t *>(y), N, K, B);
-    return true;
+                  int nph, hipStream_t s) {
+    if (nph > 1) return launch_b8_ph<T, I8, NCG, NW, CPL, KS, true>(W, sc, x, y, B, N, K, nph, s);
+    return launch_b8_ph<T, I8, NCG, NW, CPL, KS, false>(W, sc, x, y, B, N, K, 1, s);
 }
 
 template <typename T, bool I8, int NCG, int CPL, int KS>
 bool launch_b8_cpl(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
-                   hipStream_t s) {
+                   int nph, hipStream_t s) {
     switch (b8_waves(N, 4 * (I8 ? kB8RgI8 : kB8RgF16), KS)) {
-        case 14: return launch_b8_nw<T, I8, NCG, 14, CPL, KS>(W, sc, x, y, B, N, K, s);
-        case 12: return launch_b8_nw<T, I8, NCG, 12, CPL, KS>(W, sc, x, y, B, N, K, s);
-        case 8: return launch_b8_nw<T, I8, NCG, 8, CPL, KS>(W, sc, x, y, B, N, K, s);
+        case 14: return launch_b8_nw<T, I8, NCG, 14, CPL, KS>(W, sc, x, y, B, N, K, nph, s);
+        case 12: return launch_b8_nw<T, I8, NCG, 12, CPL, KS>(W, sc, x, y, B, N, K, nph, s);
+        case 8: return launch_b8_nw<T, I8, NCG, 8, CPL, KS>(W, sc, x, y, B, N, K, nph, s);
         case 7:
-            if constexpr (KS == 1) return launch_b8_nw<T, I8, NCG, 7, CPL, KS>(W, sc, x, y, B, N, K, s);
+            if constexpr (KS == 1)
+                return launch_b8_nw<T, I8, NCG, 7, CPL, KS>(W, sc, x, y, B, N, K, nph, s);
             return false;
-        default: return launch_b8_nw<T, I8, NCG, 16, CPL, KS>(W, sc, x, y, B, N, K, s);
+        default: return launch_b8_nw<T, I8, NCG, 16, CPL, KS>(W, sc, x, y, B, N, K, nph, s);
     }
 }
 
@@ -853,15 +893,17 @@ template <typename T, bool I8, int NCG>
 bool launch_b8_ncg(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                    hipStream_t s) {
     constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
-    // K split over two waves: each half a whole number of load steps (16
-    // chunks of 16 bytes per row), and the sums' LDS beside x
-    if (N < kB8SplitN && K % (I8 ? 512 : 256) == 0 &&
-        b8_lds(NCG, RG, 16, 2, K) <= static_cast<size_t>(kMaxLdsBytes))
-        return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8Split : kB8CplF16Split, 2>(W, sc, x, y, B,
-                                                                                   N, K, s);
+    if (N < kB8SplitN) {  // K split over the two waves of each row group
+        const int nph = b8_phases(NCG, RG, 2, K, I8);
+        if (nph > 0)
+            return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8Split : kB8CplF16Split, 2>(
+                W, sc, x, y, B, N, K, nph, s);
+    }
+    const int nph = b8_phases(NCG, RG, 1, K, I8);
+    if (nph == 0) return false;
     if (I8 && N < kB8SmallN)
-        return launch_b8_cpl<T, I8, NCG, kB8CplI8Small, 1>(W, sc, x, y, B, N, K, s);
-    return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8 : kB8CplF16, 1>(W, sc, x, y, B, N, K, s);
+        return launch_b8_cpl<T, I8, NCG, kB8CplI8Small, 1>(W, sc, x, y, B, N, K, nph, s);
+    return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8 : kB8CplF16, 1>(W, sc, x, y, B, N, K, nph, s);
 }
 
 template <typename T, bool I8>

@@ -636,10 +636,10 @@ def test_gemv_int8(B):
 @pytest.mark.parametrize("i8", [False, True], ids=["fp16", "int8"])
 def test_gemv_long_rows(B, K, i8):
     """Rows longer than 64 KiB of staged x: the 4x4x4 path stages up to the
-    workgroup's whole LDS (4 x 20480 x 2 bytes is exactly 160 KiB) and takes
-    batches above 4 in slices of 4 when 8 rows do not fit; the VALU path
-    stages up to 160 KiB of x per launch; 3 x 24576 falls to the 16x16x32
-    path (no staging)."""
+    workgroup's whole LDS (4 x 20480 x 2 bytes is exactly 160 KiB) and sweeps
+    K in phases, x staged one phase at a time, when the batch's rows do not
+    fit (8 x 14336, 4 x 20480 with the split-K sums, 3 x 24576); the VALU
+    path (batch 1, fp16 batch 2) stages up to 160 KiB of x per launch."""
     r = rng(700 + B + K // 1024 + (50 if i8 else 0))
     N = 1000
     x = bits(r.standard_normal((B, K)))
@@ -755,6 +755,34 @@ def test_gemv_split_k(B, N, K, i8):
                      what=f"gemv_int8 {B}x{N}x{K}")
     else:
         W = bits(r.normal(0, 0.05, (N, K)))
+        ref = orc.gemv(W, x)
+        tecoops.gemv(dev(W), dev(x), y)
+        torch.cuda.synchronize()
+        assert_close(as_f32(y), ref, what=f"gemv {B}x{N}x{K}")
+
+
+@pytest.mark.parametrize("B,N,K,i8", [(8, 1000, 14336, False), (6, 8200, 10496, False),
+                                      (8, 1000, 30720, True), (7, 8192, 21504, True),
+                                      (5, 1000, 10624, False)])
+def test_gemv_phased_x(B, N, K, i8):
+    """x that does not fit in LDS whole is staged in K phases, W still read
+    once: 2 phases with split K (8 x 14336 fp16), 2 unsplit (8200 rows), 4
+    split (int8 8 x 30720) and 3 unsplit (int8 8192 x 21504: 3 x 7168).  K =
+    10624 = 83 x 128 has no phase count that divides it into whole load
+    steps: batch 5 runs as slices of 4 and 1."""
+    r = rng(990 + B + N + K // 128 + i8)
+    x = bits(r.standard_normal((B, K)))
+    y = torch.empty((B, N), dtype=torch.float16, device="cuda")
+    if i8:
+        W = r.integers(-127, 128, (N, K), dtype=np.int8)
+        s = bits(r.uniform(0.001, 0.01, N))
+        ref = orc.gemv_int8(W, s, x)
+        tecoops.gemv_int8(dev(W), dev(s), dev(x), y)
+        torch.cuda.synchronize()
+        assert_close(as_f32(y), ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2,
+                     what=f"gemv_int8 {B}x{N}x{K}")
+    else:
+        W = bits(r.normal(0, 0.02, (N, K)))
         ref = orc.gemv(W, x)
         tecoops.gemv(dev(W), dev(x), y)
         torch.cuda.synchronize()
