@@ -761,6 +761,12 @@ constexpr long long kMaxLdsBytes = static_cast<long long>(tecoops::kLdsMax);
 // in parallelism than they save (28.7 us at 1 tile, 30.9 at 2).
 constexpr int kMfmaMinBatch16 = 3, kMfmaRT16 = 1, kMfmaWaves16 = 4;
 constexpr int kMfmaMinBatchI8 = 2, kMfmaRTI8 = 4, kMfmaWavesI8 = 8;
+// fp16 batch 2 takes the 4x4x4 path above this K: the VALU path's 2 staged
+// rows of x then leave fewer than 4 workgroups per CU.  Batch 2, VALU against
+// 4x4x4 (us): [4096, 8192] 14.1 / 16.8, [4096, 10240] 16.3-16.5 / 16.8-17.2,
+// [14336, 10240] 48.3 / 46.9, [4096, 12288] 21.2 / 18.6, [4096, 14336]
+// 23.1 / 21.7, [8192, 28672] 98.5 / 73.6.
+constexpr int kB8Batch2MinK = 10240;
 
 // VALU path shapes (rows per wave R, 16-byte W chunks per lane per K step
 // CPL), measured on the [14336, 4096] batch-1 shapes: fp16 one row per wave
@@ -980,7 +986,8 @@ extern "C" tecoopsStatus_t tecoopsGemv(tecoopsHandle_t handle, const void *weigh
     using tecoops::dev::f16;
     hipStream_t s = handle->stream;
     const bool al = tecoops::aligned(weight, 16) && tecoops::aligned(x, 16);
-    const int s8 = batch >= kMfmaMinBatch16 && al ? b8_slice(batch, k, false) : 0;
+    const bool b8 = batch >= kMfmaMinBatch16 || (batch == 2 && k > kB8Batch2MinK);
+    const int s8 = b8 && al ? b8_slice(batch, k, false) : 0;
     if (s8 > 0) {
         for (int b0 = 0; b0 < batch; b0 += s8) {
             const int nb = batch - b0 < s8 ? batch - b0 : s8;

@@ -639,7 +639,7 @@ def test_gemv_long_rows(B, K, i8):
     workgroup's whole LDS (4 x 20480 x 2 bytes is exactly 160 KiB) and sweeps
     K in phases, x staged one phase at a time, when the batch's rows do not
     fit (8 x 14336, 4 x 20480 with the split-K sums, 3 x 24576); the VALU
-    path (batch 1, fp16 batch 2) stages up to 160 KiB of x per launch."""
+    path (batch 1) stages up to 160 KiB of x per launch."""
     r = rng(700 + B + K // 1024 + (50 if i8 else 0))
     N = 1000
     x = bits(r.standard_normal((B, K)))
@@ -739,9 +739,8 @@ def test_gemv_split_k(B, N, K, i8):
     sweeping half of K, and adds their sums through LDS: halves of 1 load
     step (K = 256 fp16 / 512 int8), 9 and 5 steps (not multiples of the
     ring depth), a partial row group and waves past the last row; an int8 K
-    that is an odd number of 256-k steps (2304) takes the unsplit kernel."""
-    if B == 2 and not i8:
-        B = 3  # fp16 batch 2 runs the VALU path
+    that is an odd number of 256-k steps (2304) takes the unsplit kernel;
+    fp16 batch 2 takes this path only for K above 10240."""
     r = rng(960 + N + K + B + i8)
     x = bits(r.standard_normal((B, K)))
     y = torch.empty((B, N), dtype=torch.float16, device="cuda")
