@@ -373,6 +373,28 @@ def test_prefill_long_query_ranges(dt, H, Hkv):
         assert_close(got, ref, what=f"long query ranges H={H} Hkv={Hkv} max_q={max_q}")
 
 
+@pytest.mark.parametrize("H,Hkv", [(3, 3), (6, 2), (6, 3), (8, 2)])
+def test_prefill_output_rows_through_lds(H, Hkv):
+    """Prefill output rows leave each workgroup through LDS as runs of 1, 2
+    or 4 heads (G = 1, 3, 2, 4): ragged lengths leave partial tiles, whose
+    rows past a sequence are not written: the rows after the last sequence
+    (a sentinel tail of the output buffer) stay untouched."""
+    q_lens, kv = [1, 45, 200, 33], [1, 60, 200, 500]
+    T = sum(q_lens)
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    for dt in (orc.HALF, orc.BF16):
+        q, kc, vc, bt = make_inputs(70 + H + Hkv, H, Hkv, 128, 16, q_lens, kv, dtype=dt)
+        ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=dt)
+        tdt = torch.float16 if dt == orc.HALF else torch.bfloat16
+        buf = torch.full((T + 96, H, 128), 7.0, dtype=tdt, device="cuda")
+        tecoops.flash_attn_varlen_func(dev(q, dt), dev(kc, dt), dev(vc, dt), max(q_lens), dev(cu),
+                                       max(kv), None, dev(np.array(kv, np.int32)),
+                                       1.0 / math.sqrt(128), True, None, dev(bt), False, buf[:T])
+        torch.cuda.synchronize()
+        assert_close(as_f32(buf[:T], dt), ref, what=f"prefill rows via LDS H={H} Hkv={Hkv}")
+        assert bool((buf[T:] == 7.0).all()), "rows past the last sequence were written"
+
+
 def test_kv_len_clamped_to_block_table():
     """kv_len past block_table_dim * block_size (the reference's precondition,
     flash_attention.scpp:190) reads no block-table entry past the row: the
