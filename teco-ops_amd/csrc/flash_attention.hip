@@ -1386,6 +1386,28 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
             return prefill_hw<T, D, 12, 1, true, 96>(p, pl, s);
         }
     }
+    if constexpr (D == 64) {
+        // long query ranges: 12 waves over 192-key tiles (3 per SIMD, 136
+        // VGPRs).  bf16 H32 Hkv8 causal, µs 4-wave 64-key / 12-wave: B4 S4096
+        // 371-376 / 335, B1 S16384 1417-1421 / 1276, B2 S8192 718-733 / 654,
+        // B8 S2048 197-201 / 190; 8 waves over 128 keys 362 / 1374 / 701 / 204
+        // and 16 over 256 (128 VGPRs, spills) 342 / 1290 / 657 / 192.
+        if (pow2 && pl.rq > 1024) return prefill_hw<T, D, 12, 1, true, 192>(p, pl, s);
+    }
+    if constexpr (D == 96) {
+        // long query ranges: 12 waves over 96-key tiles (142 VGPRs).  µs
+        // 4-wave 64-key / 12-wave 96-key / 12-wave 192-key: B4 S4096 598 /
+        // 472 / 486, B1 S16384 2196 / 1771 / 1828, B8 S2048 316 / 267 / 278
+        if (pow2 && pl.rq > 1024) return prefill_hw<T, D, 12, 1, true, 96>(p, pl, s);
+    }
+    if constexpr (D == 32) {
+        // long query ranges: 8 waves over 128-key tiles.  µs 4-wave 64-key /
+        // 12-wave 192-key / 8-wave 128-key: B4 S4096 256 / 245 / 233, B1
+        // S16384 986 / 904 / 883, B8 S2048 139 / 142 / 126
+        if (pl.rq > 1024)
+            return pow2 ? prefill_hw<T, D, 8, 1, true, 128>(p, pl, s)
+                        : prefill_hw<T, D, 8, 1, false, 128>(p, pl, s);
+    }
     return pow2 ? prefill_hw<T, D, 4, 1, true>(p, pl, s) : prefill_hw<T, D, 4, 1, false>(p, pl, s);
 }
 

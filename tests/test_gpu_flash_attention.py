@@ -373,6 +373,22 @@ def test_prefill_long_query_ranges(dt, H, Hkv):
         assert_close(got, ref, what=f"long query ranges H={H} Hkv={Hkv} max_q={max_q}")
 
 
+@pytest.mark.parametrize("D", [64, 96, 32])
+@pytest.mark.parametrize("H,Hkv,bs", [(8, 2, 16), (6, 3, 8), (5, 5, 32), (8, 4, 5)])
+def test_prefill_long_query_ranges_other_head_sizes(D, H, Hkv, bs):
+    """Query ranges above 1024 rows with D = 64 (12 waves, 192-key tiles), 96
+    (12 waves, 96-key tiles) and 32 (8 waves, 128-key tiles): ragged lengths,
+    a cached prefix, a sequence shorter than one tile, GQA groups of 4, 2 and
+    1, block sizes 16, 8 (D = 64: V row groups over two cache blocks), 32 and
+    5 (the generic loader), and a max_seqlen_q hint below the longest range."""
+    q_lens, kv = [1100, 1537, 40, 1300], [1100, 2000, 900, 1300]
+    q, kc, vc, bt = make_inputs(90 + H + bs + D, H, Hkv, D, bs, q_lens, kv, dtype=orc.BF16)
+    ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=orc.BF16)
+    for max_q in (None, 1100):
+        got = run_gpu(q, kc, vc, bt, q_lens, kv, orc.BF16, max_q=max_q)
+        assert_close(got, ref, what=f"D={D} long query ranges H={H} Hkv={Hkv} bs={bs} max_q={max_q}")
+
+
 @pytest.mark.parametrize("H,Hkv", [(3, 3), (6, 2), (6, 3), (8, 2)])
 def test_prefill_output_rows_through_lds(H, Hkv):
     """Prefill output rows leave each workgroup through LDS as runs of 1, 2
