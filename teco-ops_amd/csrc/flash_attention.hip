@@ -182,10 +182,11 @@ struct TileLoader {
     static constexpr int VP = TILE + 4;
     static constexpr int ELEMS = TILE * KP + D * VP;  // one K + V^T buffer
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
-    static constexpr int KCH = TILE * CPR / NT;
+    static constexpr int KTASKS = TILE * CPR;
+    static constexpr int KCH = (KTASKS + NT - 1) / NT;
     static constexpr int VTASKS = (TILE / 4) * CPR;
     static constexpr int VPT = (VTASKS + NT - 1) / NT;
-    static_assert(D % 32 == 0 && TILE * CPR % NT == 0, "K tile must split evenly");
+    static_assert(D % 32 == 0 && TILE % 4 == 0, "whole 32-column slabs and 4-row V blocks");
     u32x4 k[KCH];
     u32x4 v[VPT][4];
     uint32_t vok;  // bit 4i+r: V row of v[i][r] is valid (below kv_limit, page in range)
@@ -203,6 +204,7 @@ struct TileLoader {
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
             const int task = tid + i * NT;
+            if (KTASKS % NT != 0 && task >= KTASKS) continue;
             bool ok;
             ko[i] = row_offset<D, POW2>(p, bt_row, head_off, j0 + task / CPR, kv_limit, ok);
         }
@@ -222,7 +224,10 @@ struct TileLoader {
             }
         }
 #pragma unroll
-        for (int i = 0; i < KCH; ++i) k[i] = load16<STREAM>(p.kc + ko[i] + ((tid + i * NT) % CPR) * 8);
+        for (int i = 0; i < KCH; ++i) {
+            if (KTASKS % NT != 0 && tid + i * NT >= KTASKS) continue;
+            k[i] = load16<STREAM>(p.kc + ko[i] + ((tid + i * NT) % CPR) * 8);
+        }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int task = tid + i * NT;
@@ -240,6 +245,7 @@ struct TileLoader {
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
             const int task = tid + i * NT;
+            if (KTASKS % NT != 0 && task >= KTASKS) continue;
             *reinterpret_cast<u32x4 *>(Ks + (task / CPR) * KP + (task % CPR) * 8) = k[i];
         }
 #pragma unroll
@@ -849,10 +855,10 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
 // query head hg*HW + w % HW of the GQA group and query rows
 // [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of TILE keys are double
 // buffered in LDS (one barrier per tile) and attended 32 * NKB keys at a time.
-// W >= 12 asks for 3 waves per SIMD (168 VGPRs); head sizes above 128 one
-// workgroup per CU (their LDS tiles allow no more); else 2.
+// W >= 12 asks for 3 waves per SIMD (168 VGPRs); head sizes above 128 with 4
+// waves one (their 4-wave tiles fill the registers), else 2.
 template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
-__global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 ? 1 : 2))
+__global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 && W < 8 ? 1 : 2))
 fa_prefill_kernel(FaParams p) {
     constexpr int QT = 32 * QSUB * (W / HW);
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -879,7 +885,7 @@ fa_prefill_kernel(FaParams p) {
 // that fa_prefill_kernel has no loop around its tile (values hoisted out of
 // a loop would stay live across the tile and cost registers).
 template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
-__global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 ? 1 : 2))
+__global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 && W < 8 ? 1 : 2))
 fa_prefill_rest_kernel(FaParams p, int first_tile) {
     constexpr int QT = 32 * QSUB * (W / HW);
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -1407,6 +1413,16 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
         if (pl.rq > 1024)
             return pow2 ? prefill_hw<T, D, 8, 1, true, 128>(p, pl, s)
                         : prefill_hw<T, D, 8, 1, false, 128>(p, pl, s);
+    }
+    if constexpr (D > 128) {
+        // 8 waves (2 per SIMD, 234 / 252 VGPRs) over 64-key tiles instead of
+        // 4 waves at one per SIMD.  µs, 4 / 8 waves: D = 192 B4 S4096 2078 /
+        // 938, B16 S1024 631 / 311, 16 x 256 rows over 4096 keys 1081 / 488,
+        // 64 x 16 over 4096 566 / 489; D = 160 1410 / 854, 443 / 284, 691 /
+        // 458, and 378 / 477 at 64 x 16 over 4096, where 4 waves stay.
+        if (D == 192 || pl.rq > 16)
+            return pow2 ? prefill_hw<T, D, 8, 1, true, 64>(p, pl, s)
+                        : prefill_hw<T, D, 8, 1, false, 64>(p, pl, s);
     }
     return pow2 ? prefill_hw<T, D, 4, 1, true>(p, pl, s) : prefill_hw<T, D, 4, 1, false>(p, pl, s);
 }

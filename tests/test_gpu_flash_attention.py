@@ -373,11 +373,13 @@ def test_prefill_long_query_ranges(dt, H, Hkv):
         assert_close(got, ref, what=f"long query ranges H={H} Hkv={Hkv} max_q={max_q}")
 
 
-@pytest.mark.parametrize("D", [64, 96, 32])
+@pytest.mark.parametrize("D", [64, 96, 32, 160, 192])
 @pytest.mark.parametrize("H,Hkv,bs", [(8, 2, 16), (6, 3, 8), (5, 5, 32), (8, 4, 5)])
 def test_prefill_long_query_ranges_other_head_sizes(D, H, Hkv, bs):
     """Query ranges above 1024 rows with D = 64 (12 waves, 192-key tiles), 96
-    (12 waves, 96-key tiles) and 32 (8 waves, 128-key tiles): ragged lengths,
+    (12 waves, 96-key tiles), 32 (8 waves, 128-key tiles) and 160 / 192 (8
+    waves, 64-key tiles, the generic loader, for D = 160 with K chunks that
+    do not split evenly over the threads): ragged lengths,
     a cached prefix, a sequence shorter than one tile, GQA groups of 4, 2 and
     1, block sizes 16, 8 (D = 64: V row groups over two cache blocks), 32 and
     5 (the generic loader), and a max_seqlen_q hint below the longest range."""
@@ -431,7 +433,8 @@ def test_head_sizes(D, dt):
     for name, H, Hkv, bs, q_lens, kv_lens in (
             ("prefill", 8, 2, 16, [130, 64], [130, 64]),
             ("decode", 16, 4, 16, [1, 1, 1], [1, 700, 2500]),
-            ("chunked", 8, 4, 5, [33, 20], [90, 20])):
+            ("chunked", 8, 4, 5, [33, 20], [90, 20]),
+            ("short chunk", 8, 2, 16, [16, 9], [300, 9])):
         case = dict(name=f"{name} D={D}", H=H, Hkv=Hkv, D=D, bs=bs, q_lens=q_lens,
                     kv_lens=kv_lens)
         check(case, dt, seed=D + len(name))
