@@ -1391,6 +1391,12 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
             if (pl.rq <= 1024) return prefill_hw<T, D, 4, 1, true, 32>(p, pl, s);
             return prefill_hw<T, D, 12, 1, true, 96>(p, pl, s);
         }
+        // other block sizes (the generic loader): the 12-wave kernel above
+        // 1024 query rows too.  Block 24, µs 4-wave 64-key / 12-wave: B4
+        // S4096 771 / 610, B1 S16384 2868-2883 / 2264-2269 (up to 1024 rows
+        // the 4-wave 32-key kernel with this loader lost: 64 x 16 rows over
+        // 4096 keys 262 / 342 us)
+        if (pl.rq > 1024) return prefill_hw<T, D, 12, 1, false, 96>(p, pl, s);
     }
     if constexpr (D == 64) {
         // long query ranges: 12 waves over 192-key tiles (3 per SIMD, 136

@@ -373,6 +373,21 @@ def test_prefill_long_query_ranges(dt, H, Hkv):
         assert_close(got, ref, what=f"long query ranges H={H} Hkv={Hkv} max_q={max_q}")
 
 
+@pytest.mark.parametrize("bs,H,Hkv", [(24, 8, 2), (5, 6, 3), (1, 5, 5)])
+def test_prefill_long_query_ranges_generic_loader(bs, H, Hkv):
+    """D = 128 query ranges above 1024 rows with block sizes that are not a
+    power of two of at least 8 take the 12-wave kernel with the generic
+    loader (one block-table lookup per row): ragged lengths, a cached prefix,
+    a sequence shorter than one tile, GQA groups of 4, 2 and 1, and a
+    max_seqlen_q hint below the longest range."""
+    q_lens, kv = [1100, 1537, 40, 1300], [1100, 2000, 900, 1300]
+    q, kc, vc, bt = make_inputs(110 + bs + H, H, Hkv, 128, bs, q_lens, kv, dtype=orc.HALF)
+    ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=orc.HALF)
+    for max_q in (None, 1100):
+        got = run_gpu(q, kc, vc, bt, q_lens, kv, orc.HALF, max_q=max_q)
+        assert_close(got, ref, what=f"bs={bs} long query ranges H={H} Hkv={Hkv} max_q={max_q}")
+
+
 @pytest.mark.parametrize("D", [64, 96, 32, 160, 192])
 @pytest.mark.parametrize("H,Hkv,bs", [(8, 2, 16), (6, 3, 8), (5, 5, 32), (8, 4, 5)])
 def test_prefill_long_query_ranges_other_head_sizes(D, H, Hkv, bs):
