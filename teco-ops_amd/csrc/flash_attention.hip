@@ -1405,12 +1405,16 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
         // B8 S2048 197-201 / 190; 8 waves over 128 keys 362 / 1374 / 701 / 204
         // and 16 over 256 (128 VGPRs, spills) 342 / 1290 / 657 / 192.
         if (pow2 && pl.rq > 1024) return prefill_hw<T, D, 12, 1, true, 192>(p, pl, s);
+        // other block sizes, generic loader: block 24, B4 S4096 433 -> 354 us
+        if (pl.rq > 1024) return prefill_hw<T, D, 12, 1, false, 192>(p, pl, s);
     }
     if constexpr (D == 96) {
         // long query ranges: 12 waves over 96-key tiles (142 VGPRs).  µs
         // 4-wave 64-key / 12-wave 96-key / 12-wave 192-key: B4 S4096 598 /
         // 472 / 486, B1 S16384 2196 / 1771 / 1828, B8 S2048 316 / 267 / 278
         if (pow2 && pl.rq > 1024) return prefill_hw<T, D, 12, 1, true, 96>(p, pl, s);
+        // other block sizes, generic loader: block 24, B4 S4096 648 -> 494 us
+        if (pl.rq > 1024) return prefill_hw<T, D, 12, 1, false, 96>(p, pl, s);
     }
     if constexpr (D == 32) {
         // long query ranges: 8 waves over 128-key tiles.  µs 4-wave 64-key /

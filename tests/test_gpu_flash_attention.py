@@ -389,15 +389,16 @@ def test_prefill_long_query_ranges_generic_loader(bs, H, Hkv):
 
 
 @pytest.mark.parametrize("D", [64, 96, 32, 160, 192])
-@pytest.mark.parametrize("H,Hkv,bs", [(8, 2, 16), (6, 3, 8), (5, 5, 32), (8, 4, 5)])
+@pytest.mark.parametrize("H,Hkv,bs", [(8, 2, 16), (6, 3, 8), (5, 5, 32), (8, 4, 5), (8, 2, 24)])
 def test_prefill_long_query_ranges_other_head_sizes(D, H, Hkv, bs):
     """Query ranges above 1024 rows with D = 64 (12 waves, 192-key tiles), 96
     (12 waves, 96-key tiles), 32 (8 waves, 128-key tiles) and 160 / 192 (8
     waves, 64-key tiles, the generic loader, for D = 160 with K chunks that
     do not split evenly over the threads): ragged lengths,
     a cached prefix, a sequence shorter than one tile, GQA groups of 4, 2 and
-    1, block sizes 16, 8 (D = 64: V row groups over two cache blocks), 32 and
-    5 (the generic loader), and a max_seqlen_q hint below the longest range."""
+    1, block sizes 16, 8 (D = 64: V row groups over two cache blocks), 32,
+    5 and 24 (the generic loader, on the same wide workgroups), and a
+    max_seqlen_q hint below the longest range."""
     q_lens, kv = [1100, 1537, 40, 1300], [1100, 2000, 900, 1300]
     q, kc, vc, bt = make_inputs(90 + H + bs + D, H, Hkv, D, bs, q_lens, kv, dtype=orc.BF16)
     ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=orc.BF16)
