@@ -25,7 +25,7 @@
 //     4-element pad) so the A operand of the PV product is two 64-bit reads.
 //     Global -> register prefetch of the next tile overlaps the current tile's
 //     MFMA work.
-//   * Prefill (D = 128, power-of-two block_size): a workgroup of 12 waves
+//   * Prefill (D = 128, block_size a multiple of 8): a workgroup of 12 waves
 //     (3 per SIMD) shares each 96-key K/V tile among up to 4 query heads of
 //     one GQA group (HW heads x (12/HW) row blocks of 32); other shapes use 4
 //     waves and 64-key tiles.  The grid walks query tiles heaviest-first and
@@ -150,14 +150,23 @@ __device__ __forceinline__ u32x4 load16(const uint16_t *p) {
 // beyond kv_limit, and rows whose page id is out of range, are redirected to
 // a row that exists and reported through ok = false; the caller zeroes V for
 // them and masks K.
-template <int D, bool POW2>
+// Block-size modes of the loaders (a template argument, so that the power
+// of two case keeps its shift): 0 any block_size (one block-table lookup per
+// key row), 1 a power of two >= 8, 2 another multiple of 8.  Cache block of
+// key row kv: a shift in mode 1, a division otherwise.
+template <int BSM>
+__device__ __forceinline__ int block_of(const FaParams &p, int kv) {
+    return BSM == 1 ? kv >> p.lbs : kv / p.bs;
+}
+
+template <int D, int BSM>
 __device__ __forceinline__ long long row_offset(const FaParams &p, const int *bt_row,
                                                 long long head_off, int kv, int kv_limit,
                                                 bool &ok) {
     ok = kv < kv_limit;
     const int kvs = ok ? kv : 0;
     int blk, off;
-    if (POW2) {
+    if (BSM == 1) {
         blk = kvs >> p.lbs;
         off = kvs & (p.bs - 1);
     } else {
@@ -176,7 +185,7 @@ __device__ __forceinline__ long long row_offset(const FaParams &p, const int *bt
 // 16-byte chunks of K are dealt to the threads in order (chunk tid + i*NT is
 // row / column (tid + i*NT) / (D/8), % (D/8)); each thread also owns VPT
 // (4-row x 8-column) blocks of V.
-template <int D, int TILE, int NT, bool POW2, bool STREAM = false>
+template <int D, int TILE, int NT, int BSM, bool STREAM = false>
 struct TileLoader {
     static constexpr int KP = D + 8;
     static constexpr int VP = TILE + 4;
@@ -206,7 +215,7 @@ struct TileLoader {
             const int task = tid + i * NT;
             if (KTASKS % NT != 0 && task >= KTASKS) continue;
             bool ok;
-            ko[i] = row_offset<D, POW2>(p, bt_row, head_off, j0 + task / CPR, kv_limit, ok);
+            ko[i] = row_offset<D, BSM>(p, bt_row, head_off, j0 + task / CPR, kv_limit, ok);
         }
         // Invalid V rows are zeroed in store(), so the wave does not wait for
         // the loads here.
@@ -219,7 +228,7 @@ struct TileLoader {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 bool ok;
-                vo[i][r] = row_offset<D, POW2>(p, bt_row, head_off, j0 + 4 * rg + r, kv_limit, ok);
+                vo[i][r] = row_offset<D, BSM>(p, bt_row, head_off, j0 + 4 * rg + r, kv_limit, ok);
                 vok |= (ok ? 1u : 0u) << (4 * i + r);
             }
         }
@@ -273,7 +282,7 @@ struct TileLoader {
     }
 };
 
-// Loader for D = 128 and a power-of-two block_size >= 8.  Wave w stages rows
+// Loader for D = 128 and a block_size that is a multiple of 8.  Wave w stages rows
 // [w*RW, (w+1)*RW) of the tile.  Each K load instruction covers 4 aligned rows
 // (16 lanes x 16 bytes per row) and each V load instruction 8 aligned rows
 // (lane l: rows 2*(l%4) + {0,1}, column block l/4), so the cache block
@@ -282,7 +291,7 @@ struct TileLoader {
 // global loads never wait for it.  Same LDS layout as TileLoader: K [TILE][D +
 // 8], V^T [D][TILE + 4].  load() must be called for consecutive tiles after
 // one prefetch() of the first.
-template <int TILE, int W, bool STREAM = false>
+template <int TILE, int W, int BSM, bool STREAM = false>
 struct PagedLoader128 {
     static constexpr int D = 128;
     static constexpr int KP = D + 8;
@@ -307,7 +316,7 @@ struct PagedLoader128 {
         // load, so waiting for it never waits for the K/V vector loads in
         // flight (a vector load here would, under s_waitcnt vmcnt).
         const auto *bt4 = (const __attribute__((address_space(4))) int *)(bt_row);
-        return row0 < kv_limit ? bt4[row0 >> p.lbs] : 0;
+        return row0 < kv_limit ? bt4[block_of<BSM>(p, row0)] : 0;
     }
 
     // Element offset of the group's first row (page 0 when its id is out of range).
@@ -315,7 +324,8 @@ struct PagedLoader128 {
                                                            int row0, int page) {
         if (page < 0 || page >= p.num_blocks) page = 0;
         return static_cast<long long>(page) * p.page_stride + head_off +
-               static_cast<long long>(row0 & (p.bs - 1)) * D;
+               static_cast<long long>(BSM == 1 ? row0 & (p.bs - 1)
+                                                : row0 - block_of<BSM>(p, row0) * p.bs) * D;
     }
 
     __device__ __forceinline__ void prefetch(const FaParams &p, const int *bt_row, int j0,
@@ -389,7 +399,7 @@ struct PagedLoader128 {
 // one per half-wave (lane l: rows 8*(l/32) + 2*(l%4) + {0,1}, column block
 // (l/4)%8), whose cache blocks are looked up separately, so block sizes of 8
 // work too.
-template <int TILE, int W, bool STREAM = false>
+template <int TILE, int W, int BSM, bool STREAM = false>
 struct PagedLoader64 {
     static constexpr int D = 64;
     static constexpr int KP = D + 8;
@@ -409,11 +419,11 @@ struct PagedLoader64 {
         const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
         for (int i = 0; i < KI; ++i)
-            pg[i] = PagedLoader128<TILE, W, STREAM>::group_page(p, bt_row, j0 + w * RW + 8 * i,
+            pg[i] = PagedLoader128<TILE, W, BSM, STREAM>::group_page(p, bt_row, j0 + w * RW + 8 * i,
                                                                 kv_limit);
 #pragma unroll
         for (int i = 0; i < 2 * VI; ++i)
-            pg[KI + i] = PagedLoader128<TILE, W, STREAM>::group_page(p, bt_row,
+            pg[KI + i] = PagedLoader128<TILE, W, BSM, STREAM>::group_page(p, bt_row,
                                                                      j0 + w * RW + 8 * i, kv_limit);
     }
 
@@ -421,7 +431,8 @@ struct PagedLoader64 {
                                                            int row0, int page) {
         if (page < 0 || page >= p.num_blocks) page = 0;
         return static_cast<long long>(page) * p.page_stride + head_off +
-               static_cast<long long>(row0 & (p.bs - 1)) * D;
+               static_cast<long long>(BSM == 1 ? row0 & (p.bs - 1)
+                                                : row0 - block_of<BSM>(p, row0) * p.bs) * D;
     }
 
     __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
@@ -482,7 +493,7 @@ struct PagedLoader64 {
 // instruction covers 4 aligned rows on lanes 0-47 and a V instruction 8
 // aligned rows (lane l: rows 2*(l%4) + {0,1}, column block l/4) on lanes
 // 0-47; lanes 48-63 repeat lane 47's load and store nothing.
-template <int TILE, int W, bool STREAM = false>
+template <int TILE, int W, int BSM, bool STREAM = false>
 struct PagedLoader96 {
     static constexpr int D = 96;
     static constexpr int KP = D + 8;
@@ -502,11 +513,11 @@ struct PagedLoader96 {
         const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
         for (int i = 0; i < KI; ++i)
-            pg[i] = PagedLoader128<TILE, W, STREAM>::group_page(p, bt_row, j0 + w * RW + 4 * i,
+            pg[i] = PagedLoader128<TILE, W, BSM, STREAM>::group_page(p, bt_row, j0 + w * RW + 4 * i,
                                                                 kv_limit);
 #pragma unroll
         for (int i = 0; i < VI; ++i)
-            pg[KI + i] = PagedLoader128<TILE, W, STREAM>::group_page(p, bt_row,
+            pg[KI + i] = PagedLoader128<TILE, W, BSM, STREAM>::group_page(p, bt_row,
                                                                      j0 + w * RW + 8 * i, kv_limit);
     }
 
@@ -514,7 +525,8 @@ struct PagedLoader96 {
                                                            int row0, int page) {
         if (page < 0 || page >= p.num_blocks) page = 0;
         return static_cast<long long>(page) * p.page_stride + head_off +
-               static_cast<long long>(row0 & (p.bs - 1)) * D;
+               static_cast<long long>(BSM == 1 ? row0 & (p.bs - 1)
+                                                : row0 - block_of<BSM>(p, row0) * p.bs) * D;
     }
 
     __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
@@ -571,21 +583,33 @@ struct PagedLoader96 {
 
 // Loader choice: the uniform-page loader when it applies, else TileLoader.
 // STREAM marks K/V read once per launch (decode): non-temporal loads.
-template <int D, int TILE, int W, bool POW2, bool STREAM = false>
+template <int D, int TILE, int W, int BSM, bool STREAM = false>
 struct LoaderSel {
-    using type = TileLoader<D, TILE, W * 64, POW2, STREAM>;
+    using type = TileLoader<D, TILE, W * 64, BSM, STREAM>;
 };
 template <int TILE, int W, bool STREAM>
-struct LoaderSel<128, TILE, W, true, STREAM> {
-    using type = PagedLoader128<TILE, W, STREAM>;
+struct LoaderSel<128, TILE, W, 1, STREAM> {
+    using type = PagedLoader128<TILE, W, 1, STREAM>;
 };
 template <int TILE, int W, bool STREAM>
-struct LoaderSel<64, TILE, W, true, STREAM> {
-    using type = PagedLoader64<TILE, W, STREAM>;
+struct LoaderSel<128, TILE, W, 2, STREAM> {
+    using type = PagedLoader128<TILE, W, 2, STREAM>;
 };
 template <int TILE, int W, bool STREAM>
-struct LoaderSel<96, TILE, W, true, STREAM> {
-    using type = PagedLoader96<TILE, W, STREAM>;
+struct LoaderSel<64, TILE, W, 1, STREAM> {
+    using type = PagedLoader64<TILE, W, 1, STREAM>;
+};
+template <int TILE, int W, bool STREAM>
+struct LoaderSel<64, TILE, W, 2, STREAM> {
+    using type = PagedLoader64<TILE, W, 2, STREAM>;
+};
+template <int TILE, int W, bool STREAM>
+struct LoaderSel<96, TILE, W, 1, STREAM> {
+    using type = PagedLoader96<TILE, W, 1, STREAM>;
+};
+template <int TILE, int W, bool STREAM>
+struct LoaderSel<96, TILE, W, 2, STREAM> {
+    using type = PagedLoader96<TILE, W, 2, STREAM>;
 };
 
 template <typename T> struct Ones2;
@@ -737,12 +761,12 @@ constexpr size_t prefill_lds_bytes() {
 // One query tile [q0, q0 + QT) of workgroup (b, kv head kvh, head group hg):
 // the body of fa_prefill_kernel.  Ends with a barrier, so the LDS tile
 // buffers can be refilled by the next call.
-template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
+template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
 __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, int b, int kvh,
                                              int hg, long long q_off, int L, int S, int q0) {
     constexpr int NKB = TILE % 64 == 0 ? 2 : 1;
     constexpr int KB = 32 * NKB;
-    using Loader = typename LoaderSel<D, TILE, W, POW2>::type;
+    using Loader = typename LoaderSel<D, TILE, W, BSM>::type;
     constexpr int KP = Loader::KP, VP = Loader::VP;
     constexpr int WROWS = 32 * QSUB;
     constexpr int QT = WROWS * (W / HW);
@@ -857,7 +881,7 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
 // buffered in LDS (one barrier per tile) and attended 32 * NKB keys at a time.
 // W >= 12 asks for 3 waves per SIMD (168 VGPRs); head sizes above 128 with 4
 // waves one (their 4-wave tiles fill the registers), else 2.
-template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
+template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
 __global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 && W < 8 ? 1 : 2))
 fa_prefill_kernel(FaParams p) {
     constexpr int QT = 32 * QSUB * (W / HW);
@@ -873,7 +897,7 @@ fa_prefill_kernel(FaParams p) {
     seq_info(p, b, q_off, L);
     const int tile = gridDim.y - 1 - blockIdx.y;  // heaviest causal tiles first
     if (tile * QT >= L) return;
-    prefill_tile<T, D, W, HW, QSUB, POW2, TILE>(p, lds, b, kvh, hg, q_off, L, kv_len(p, b),
+    prefill_tile<T, D, W, HW, QSUB, BSM, TILE>(p, lds, b, kvh, hg, q_off, L, kv_len(p, b),
                                                 tile * QT);
 }
 
@@ -884,7 +908,7 @@ fa_prefill_kernel(FaParams p) {
 // holds, every workgroup finds no tile and exits.  A kernel of its own, so
 // that fa_prefill_kernel has no loop around its tile (values hoisted out of
 // a loop would stay live across the tile and cost registers).
-template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
+template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
 __global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 && W < 8 ? 1 : 2))
 fa_prefill_rest_kernel(FaParams p, int first_tile) {
     constexpr int QT = 32 * QSUB * (W / HW);
@@ -900,7 +924,7 @@ fa_prefill_rest_kernel(FaParams p, int first_tile) {
     seq_info(p, b, q_off, L);
     const int S = kv_len(p, b);
     for (int t = first_tile; t * QT < L; ++t)
-        prefill_tile<T, D, W, HW, QSUB, POW2, TILE>(p, lds, b, kvh, hg, q_off, L, S, t * QT);
+        prefill_tile<T, D, W, HW, QSUB, BSM, TILE>(p, lds, b, kvh, hg, q_off, L, S, t * QT);
 }
 
 // ----------------------------------------------------------------- decode
@@ -918,11 +942,11 @@ constexpr size_t decode_lds_bytes() {
 // [32w, 32w + 32) of each 128-key tile.  Leaves each wave's partial state in
 // LDS, after a barrier: max lm[4][32], sum ll[4][32] and unnormalised O
 // lo[4][32][D] (fp32, over the tile buffers).
-template <typename T, int D, bool POW2>
+template <typename T, int D, int BSM>
 __device__ __forceinline__ void decode_pass(const FaParams &p, uint16_t *smem, int b, int kvh,
                                             long long q_off, int L, int S, int kv_lo, int kv_hi,
                                             int rq, int r0) {
-    using Loader = typename LoaderSel<D, kDecTile, 4, POW2, true>::type;
+    using Loader = typename LoaderSel<D, kDecTile, 4, BSM, true>::type;
     constexpr int KP = Loader::KP, VP = Loader::VP;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 5, r32 = lane & 31;
@@ -1147,7 +1171,7 @@ __device__ bool decode_item(const FaParams &p, int i, int &b, int &kvh, int &spl
     return true;
 }
 
-template <typename T, int D, bool POW2>
+template <typename T, int D, int BSM>
 __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) fa_decode_kernel(FaParams p) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     int b, kvh, split, L, S;
@@ -1171,7 +1195,7 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) fa_decode_kernel(FaParam
         if (split != 0) return;
         const int rq = 32 / p.G;
         for (int r0 = 0; r0 < L; r0 += rq) {
-            decode_pass<T, D, POW2>(p, smem, b, kvh, q_off, L, S, 0, S, rq, r0);
+            decode_pass<T, D, BSM>(p, smem, b, kvh, q_off, L, S, 0, S, rq, r0);
             merge_waves<D>(smem, p.G * rq, [&](int c, int d, float acc, float, float l) {
                 const int hl = c / rq, row = r0 + c % rq;
                 if (row >= L) return;
@@ -1184,7 +1208,7 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) fa_decode_kernel(FaParam
     }
     const int kv_lo = split * p.split_len;
     const int kv_hi = split == decode_items(p, L, S) - 1 ? S : min(S, kv_lo + p.split_len);
-    decode_pass<T, D, POW2>(p, smem, b, kvh, q_off, L, S, kv_lo, kv_hi, p.rq, 0);
+    decode_pass<T, D, BSM>(p, smem, b, kvh, q_off, L, S, kv_lo, kv_hi, p.rq, 0);
     if (p.max_splits == 1) {
         // one split per sequence: the rows are final here, normalised with
         // the merge kernel's arithmetic (the reciprocal of l, then a product),
@@ -1332,11 +1356,11 @@ size_t workspace_bytes(const Plan &pl, int batch, int Hkv, int D) {
 // Prefill over a grid of ceil(q_hint / QT) query tiles per (b, kv head, head
 // group), then, unless q_hint already bounds every q_len (it is at least the
 // total q length), fa_prefill_rest_kernel for the tiles past the grid.
-template <typename T, int D, int W, int HW, int QSUB, bool POW2, int TILE>
+template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
 tecoopsStatus_t launch_prefill(const FaParams &p, const Plan &pl, hipStream_t s) {
     constexpr int QT = 32 * QSUB * (W / HW);
-    auto *kern = &fa_prefill_kernel<T, D, W, HW, QSUB, POW2, TILE>;
-    auto *rest = &fa_prefill_rest_kernel<T, D, W, HW, QSUB, POW2, TILE>;
+    auto *kern = &fa_prefill_kernel<T, D, W, HW, QSUB, BSM, TILE>;
+    auto *rest = &fa_prefill_rest_kernel<T, D, W, HW, QSUB, BSM, TILE>;
     const size_t lds = prefill_lds_bytes<D, TILE, W, HW, QSUB>();
     if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds) ||
         !tecoops::reserve_lds(reinterpret_cast<const void *>(rest), lds))
@@ -1352,20 +1376,27 @@ tecoopsStatus_t launch_prefill(const FaParams &p, const Plan &pl, hipStream_t s)
     return TECOOPS_STATUS_SUCCESS;
 }
 
-template <typename T, int D, int W, int QSUB, bool POW2, int TILE = 64>
+template <typename T, int D, int W, int QSUB, int BSM, int TILE = 64>
 tecoopsStatus_t prefill_hw(const FaParams &p, const Plan &pl, hipStream_t s) {
     const int G = p.G;
-    if (G % 4 == 0) return launch_prefill<T, D, W, 4, QSUB, POW2, TILE>(p, pl, s);
-    if (G % 2 == 0) return launch_prefill<T, D, W, 2, QSUB, POW2, TILE>(p, pl, s);
-    return launch_prefill<T, D, W, 1, QSUB, POW2, TILE>(p, pl, s);
+    if (G % 4 == 0) return launch_prefill<T, D, W, 4, QSUB, BSM, TILE>(p, pl, s);
+    if (G % 2 == 0) return launch_prefill<T, D, W, 2, QSUB, BSM, TILE>(p, pl, s);
+    return launch_prefill<T, D, W, 1, QSUB, BSM, TILE>(p, pl, s);
 }
 
 template <typename T, int D>
 tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
-    const bool pow2 = p.lbs >= 3;  // power of two and >= 8: uniform-page loader
+    // Block-size mode (block_of): the uniform-page loaders take block sizes
+    // that are multiples of 8 (their 4- and 8-row groups start at multiples
+    // of 8, so none crosses a cache block), powers of two with a shift
+    const int bsm = p.lbs >= 3 ? 1 : (p.bs % 8 == 0 ? 2 : 0);
     if (pl.decode) {
         const size_t lds = decode_lds_bytes<D>();
-        auto *kern = pow2 ? &fa_decode_kernel<T, D, true> : &fa_decode_kernel<T, D, false>;
+        // mode 2 only where a uniform-page loader exists
+        const int dm = (bsm == 2 && !(D == 64 || D == 96 || D == 128)) ? 0 : bsm;
+        auto *kern = dm == 1   ? &fa_decode_kernel<T, D, 1>
+                     : dm == 2 ? &fa_decode_kernel<T, D, 2>
+                               : &fa_decode_kernel<T, D, 0>;
         if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds)) return TECOOPS_STATUS_INTERNAL_ERROR;
         dim3 grid(p.batch * p.Hkv, pl.max_splits);
         hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, p);
@@ -1387,16 +1418,20 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
         // 278, 64 x 32 408 / 249, 16 x 256 384 / 354, 8 x 512 341 / 327,
         // prefill 16 x 1024 220 / 206, 4 x 4096 643 / 689, 1 x 16384 2162 /
         // 2370.
-        if (pow2) {
-            if (pl.rq <= 1024) return prefill_hw<T, D, 4, 1, true, 32>(p, pl, s);
-            return prefill_hw<T, D, 12, 1, true, 96>(p, pl, s);
+        if (bsm == 1) {
+            if (pl.rq <= 1024) return prefill_hw<T, D, 4, 1, 1, 32>(p, pl, s);
+            return prefill_hw<T, D, 12, 1, 1, 96>(p, pl, s);
+        }
+        if (bsm == 2) {  // block 24, µs mode 0 / 2: B4 S4096 606 / 587, B16 S1024 244 / 208
+            if (pl.rq <= 1024) return prefill_hw<T, D, 4, 1, 2, 32>(p, pl, s);
+            return prefill_hw<T, D, 12, 1, 2, 96>(p, pl, s);
         }
         // other block sizes (the generic loader): the 12-wave kernel above
         // 1024 query rows too.  Block 24, µs 4-wave 64-key / 12-wave: B4
         // S4096 771 / 610, B1 S16384 2868-2883 / 2264-2269 (up to 1024 rows
         // the 4-wave 32-key kernel with this loader lost: 64 x 16 rows over
         // 4096 keys 262 / 342 us)
-        if (pl.rq > 1024) return prefill_hw<T, D, 12, 1, false, 96>(p, pl, s);
+        if (pl.rq > 1024) return prefill_hw<T, D, 12, 1, 0, 96>(p, pl, s);
     }
     if constexpr (D == 64) {
         // long query ranges: 12 waves over 192-key tiles (3 per SIMD, 136
@@ -1404,25 +1439,25 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
         // 371-376 / 335, B1 S16384 1417-1421 / 1276, B2 S8192 718-733 / 654,
         // B8 S2048 197-201 / 190; 8 waves over 128 keys 362 / 1374 / 701 / 204
         // and 16 over 256 (128 VGPRs, spills) 342 / 1290 / 657 / 192.
-        if (pow2 && pl.rq > 1024) return prefill_hw<T, D, 12, 1, true, 192>(p, pl, s);
+        if (bsm == 1 && pl.rq > 1024) return prefill_hw<T, D, 12, 1, 1, 192>(p, pl, s);
         // other block sizes, generic loader: block 24, B4 S4096 433 -> 354 us
-        if (pl.rq > 1024) return prefill_hw<T, D, 12, 1, false, 192>(p, pl, s);
+        if (pl.rq > 1024) return prefill_hw<T, D, 12, 1, 0, 192>(p, pl, s);
     }
     if constexpr (D == 96) {
         // long query ranges: 12 waves over 96-key tiles (142 VGPRs).  µs
         // 4-wave 64-key / 12-wave 96-key / 12-wave 192-key: B4 S4096 598 /
         // 472 / 486, B1 S16384 2196 / 1771 / 1828, B8 S2048 316 / 267 / 278
-        if (pow2 && pl.rq > 1024) return prefill_hw<T, D, 12, 1, true, 96>(p, pl, s);
+        if (bsm == 1 && pl.rq > 1024) return prefill_hw<T, D, 12, 1, 1, 96>(p, pl, s);
         // other block sizes, generic loader: block 24, B4 S4096 648 -> 494 us
-        if (pl.rq > 1024) return prefill_hw<T, D, 12, 1, false, 96>(p, pl, s);
+        if (pl.rq > 1024) return prefill_hw<T, D, 12, 1, 0, 96>(p, pl, s);
     }
     if constexpr (D == 32) {
         // long query ranges: 8 waves over 128-key tiles.  µs 4-wave 64-key /
         // 12-wave 192-key / 8-wave 128-key: B4 S4096 256 / 245 / 233, B1
         // S16384 986 / 904 / 883, B8 S2048 139 / 142 / 126
         if (pl.rq > 1024)
-            return pow2 ? prefill_hw<T, D, 8, 1, true, 128>(p, pl, s)
-                        : prefill_hw<T, D, 8, 1, false, 128>(p, pl, s);
+            return bsm == 1 ? prefill_hw<T, D, 8, 1, 1, 128>(p, pl, s)
+                            : prefill_hw<T, D, 8, 1, 0, 128>(p, pl, s);
     }
     if constexpr (D > 128) {
         // 8 waves (2 per SIMD, 234 / 252 VGPRs) over 64-key tiles instead of
@@ -1431,10 +1466,10 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
         // 64 x 16 over 4096 566 / 489; D = 160 1410 / 854, 443 / 284, 691 /
         // 458, and 378 / 477 at 64 x 16 over 4096, where 4 waves stay.
         if (D == 192 || pl.rq > 16)
-            return pow2 ? prefill_hw<T, D, 8, 1, true, 64>(p, pl, s)
-                        : prefill_hw<T, D, 8, 1, false, 64>(p, pl, s);
+            return bsm == 1 ? prefill_hw<T, D, 8, 1, 1, 64>(p, pl, s)
+                            : prefill_hw<T, D, 8, 1, 0, 64>(p, pl, s);
     }
-    return pow2 ? prefill_hw<T, D, 4, 1, true>(p, pl, s) : prefill_hw<T, D, 4, 1, false>(p, pl, s);
+    return bsm == 1 ? prefill_hw<T, D, 4, 1, 1>(p, pl, s) : prefill_hw<T, D, 4, 1, 0>(p, pl, s);
 }
 
 // Head sizes the kernels are built for: the reference takes the head size as

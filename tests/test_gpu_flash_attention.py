@@ -118,11 +118,18 @@ def test_reference_cases_bf16(case):
     check(case, orc.BF16, seed=2)
 
 
-@pytest.mark.parametrize("bs", [16, 1, 5, 64])
+@pytest.mark.parametrize("bs", [16, 1, 5, 64, 24, 40])
 def test_block_sizes(bs):
+    """Powers of two of at least 8 take the page-uniform loaders with a shift,
+    other multiples of 8 (24, 40) the same loaders with a division, the rest
+    (1, 5) the per-row loader: prefill and chunks, then a decode step over
+    several splits."""
     case = dict(name=f"bs{bs}", H=8, Hkv=2, D=128, bs=bs, q_lens=[1, 70, 129],
                 kv_lens=[200, 70, 300])
     check(case, orc.BF16, seed=bs)
+    case = dict(name=f"bs{bs} decode", H=8, Hkv=2, D=128, bs=bs, q_lens=[1, 1, 1],
+                kv_lens=[200, 3001, 70])
+    check(case, orc.BF16, seed=bs + 1)
 
 
 def test_non_causal_and_chunk_longer_than_kv():
@@ -456,12 +463,13 @@ def test_head_sizes(D, dt):
         check(case, dt, seed=D + len(name))
 
 
-@pytest.mark.parametrize("bs", [8, 16, 32, 5])
+@pytest.mark.parametrize("bs", [8, 16, 32, 5, 24])
 @pytest.mark.parametrize("D", [64, 96])
 def test_head_size_64_96_block_sizes(D, bs):
     """D = 64 and 96 with block sizes 8 (for D = 64 the page-uniform loader's
-    V groups of 16 rows then span two cache blocks), 16, 32 and 5 (the
-    generic loader): prefill with a cached prefix, decode and a chunk."""
+    V groups of 16 rows then span two cache blocks), 16, 32, 24 (the same
+    loaders with a division) and 5 (the generic loader): prefill with a
+    cached prefix, decode and a chunk."""
     for name, H, Hkv, q_lens, kv_lens in (("prefill", 8, 2, [130, 77], [300, 77]),
                                           ("decode", 16, 4, [1, 1, 1], [3, 700, 2500]),
                                           ("chunk", 8, 4, [33, 20], [90, 20])):
