@@ -1392,11 +1392,10 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
     const int bsm = p.lbs >= 3 ? 1 : (p.bs % 8 == 0 ? 2 : 0);
     if (pl.decode) {
         const size_t lds = decode_lds_bytes<D>();
-        // mode 2 only where a uniform-page loader exists
-        const int dm = (bsm == 2 && !(D == 64 || D == 96 || D == 128)) ? 0 : bsm;
-        auto *kern = dm == 1   ? &fa_decode_kernel<T, D, 1>
-                     : dm == 2 ? &fa_decode_kernel<T, D, 2>
-                               : &fa_decode_kernel<T, D, 0>;
+        // mode 2 only where a uniform-page loader exists (else mode 0)
+        auto *kern = bsm == 1 ? &fa_decode_kernel<T, D, 1> : &fa_decode_kernel<T, D, 0>;
+        if constexpr (D == 64 || D == 96 || D == 128)
+            if (bsm == 2) kern = &fa_decode_kernel<T, D, 2>;
         if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds)) return TECOOPS_STATUS_INTERNAL_ERROR;
         dim3 grid(p.batch * p.Hkv, pl.max_splits);
         hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, p);

@@ -457,7 +457,8 @@ def test_head_sizes(D, dt):
             ("prefill", 8, 2, 16, [130, 64], [130, 64]),
             ("decode", 16, 4, 16, [1, 1, 1], [1, 700, 2500]),
             ("chunked", 8, 4, 5, [33, 20], [90, 20]),
-            ("short chunk", 8, 2, 16, [16, 9], [300, 9])):
+            ("short chunk", 8, 2, 16, [16, 9], [300, 9]),
+            ("decode bs24", 16, 4, 24, [1, 1, 1], [1, 700, 2500])):
         case = dict(name=f"{name} D={D}", H=H, Hkv=Hkv, D=D, bs=bs, q_lens=q_lens,
                     kv_lens=kv_lens)
         check(case, dt, seed=D + len(name))
