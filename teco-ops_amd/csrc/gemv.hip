@@ -471,7 +471,7 @@ gemv_i8_mfma_kernel(const int8_t *__restrict__ W, const uint16_t *__restrict__ s
 // values.  The 16 blocks hold partial sums over disjoint k; once the wave has
 // covered K they are added across lanes l, l + 4, ..., l + 60 without LDS
 // (DPP row rotations by 4 and 8, then the row-pair and half-wave permlane
-// swaps).  Unless K is split over two waves (small N), no cross-wave
+// swaps).  Unless K is split over 2 or 4 waves (small N), no cross-wave
 // reduction or barrier follows the staging of x.
 //   x is staged in LDS as [4*NCG][K] 16-bit values with the 16-byte chunks of
 //   row i XOR-swizzled by 4*(i % 4) inside each 256-byte run, so that the
@@ -512,7 +512,7 @@ __device__ __forceinline__ int xs_chunk(int row, int c, int K) {
 // (1 for B <= 4, else 2).  RG: groups of 4 rows per wave, which share each x
 // read from LDS.  CPL: load steps a lane keeps in flight (RG loads each).
 // KS: waves per row group, each sweeping 1/KS of K; their sums meet in LDS
-// (KS = 2 when N is small, so that the grid still has enough waves).
+// (KS = 2 or 4 when N is small, so that the grid still has enough waves).
 // PHASED: K is swept in nph equal phases, x staged in LDS one phase at a
 // time (rows whose whole x does not fit in LDS); W is still read once.
 template <typename T, bool I8, int NCG, int RG, int NW, int CPL, int KS, bool PHASED>
@@ -666,12 +666,15 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
                 __syncthreads();
             });
     }
-    if constexpr (KS == 2) {
-        // part 1 hands its sums to part 0 through LDS past the staged x:
-        // value e of lane l of row group gw at red[e][gw * 64 + l], so that
-        // the 64 lanes of a wave touch 64 consecutive words per value
-        float *mine = reinterpret_cast<float *>(xs + 4 * NCG * kp) + gw * 64 + lane;
-        if (part == 1) {
+    if constexpr (KS > 1) {
+        // parts 1 .. KS-1 hand their sums to part 0 through LDS past the
+        // staged x: value e of lane l of row group gw from part pt at
+        // red[pt - 1][e][gw * 64 + l], so that the 64 lanes of a wave touch
+        // 64 consecutive words per value
+        constexpr int NV = RG * NCG * 4;
+        const float *red = reinterpret_cast<const float *>(xs + 4 * NCG * kp) + gw * 64 + lane;
+        if (part > 0) {
+            float *mine = const_cast<float *>(red) + (part - 1) * NV * GW * 64;
 #pragma unroll
             for (int g = 0; g < RG; ++g)
 #pragma unroll
@@ -681,14 +684,16 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
                         mine[((g * NCG + cg) * 4 + v) * GW * 64] = acc[g][cg][v];
         }
         __syncthreads();
-        if (part == 1) return;
+        if (part > 0) return;
 #pragma unroll
-        for (int g = 0; g < RG; ++g)
+        for (int pt = 1; pt < KS; ++pt)
 #pragma unroll
-            for (int cg = 0; cg < NCG; ++cg)
+            for (int g = 0; g < RG; ++g)
 #pragma unroll
-                for (int v = 0; v < 4; ++v)
-                    acc[g][cg][v] += mine[((g * NCG + cg) * 4 + v) * GW * 64];
+                for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        acc[g][cg][v] += red[((pt - 1) * NV + (g * NCG + cg) * 4 + v) * GW * 64];
     }
     if (n0 >= N) return;
     // add the 16 blocks' partial sums (lanes r, r + 4, ..., r + 60: rotations
@@ -797,6 +802,11 @@ constexpr int kB8SmallN = 8192, kB8CplI8Small = 8;
 // N = 4096, K = 4096, batch 8: fp16 11.0 -> 9.5 us.  Loads in flight per
 // lane: 8 fp16 / 4 int8 (4 / 8 and 16 / 2 were slower at most shapes).
 constexpr int kB8SplitN = 8192, kB8CplF16Split = 8, kB8CplI8Split = 4;
+// Up to 4096 rows with rows of at least 8192 values, four waves share each
+// row group (2 int8 / 4 fp16 steps in flight per lane): [4096, 14336] batch
+// 5 / 8, int8 17.7 / 18.5 -> 16.5 / 17.3 us, fp16 25.0 / 25.7 -> 24.2 /
+// 25.1 us.  At N = 6144 (batch 8: 11.5 -> 14.0 us) and K = 4096 it lost.
+constexpr int kB8Split4N = 4096, kB8Split4MinK = 8192, kB8CplF16Split4 = 4, kB8CplI8Split4 = 2;
 constexpr int kB8MaxBatch = 8;
 
 // Rows of x per launch of the VALU path (x [rows, K] staged in LDS): up to 8.
@@ -830,10 +840,10 @@ int b8_waves(int N, int rows_per_wave, int ks) {
 }
 
 // LDS bytes of the 4x4x4 path: staged x (kp values of 4 * ncg rows), plus
-// the partial sums handed between the K halves when ks = 2.
+// the partial sums the ks - 1 other parts of each row group hand to part 0.
 size_t b8_lds(int ncg, int rg, int nw, int ks, int kp) {
     return 4 * ncg * static_cast<size_t>(kp) * 2 +
-           (ks == 2 ? static_cast<size_t>(rg) * ncg * 4 * (nw / 2) * 64 * 4 : 0);
+           static_cast<size_t>(rg) * ncg * 4 * (nw / ks) * 64 * 4 * (ks - 1);
 }
 
 // Phases the 4x4x4 path sweeps K in (x staged one phase at a time): the
@@ -884,7 +894,10 @@ template <typename T, bool I8, int NCG, int CPL, int KS>
 bool launch_b8_cpl(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                    int nph, hipStream_t s) {
     switch (b8_waves(N, 4 * (I8 ? kB8RgI8 : kB8RgF16), KS)) {
-        case 14: return launch_b8_nw<T, I8, NCG, 14, CPL, KS>(W, sc, x, y, B, N, K, nph, s);
+        case 14:
+            if constexpr (14 % KS == 0)
+                return launch_b8_nw<T, I8, NCG, 14, CPL, KS>(W, sc, x, y, B, N, K, nph, s);
+            return false;
         case 12: return launch_b8_nw<T, I8, NCG, 12, CPL, KS>(W, sc, x, y, B, N, K, nph, s);
         case 8: return launch_b8_nw<T, I8, NCG, 8, CPL, KS>(W, sc, x, y, B, N, K, nph, s);
         case 7:
@@ -899,6 +912,12 @@ template <typename T, bool I8, int NCG>
 bool launch_b8_ncg(const void *W, const void *sc, const void *x, void *y, int B, int N, int K,
                    hipStream_t s) {
     constexpr int RG = I8 ? kB8RgI8 : kB8RgF16;
+    if (N <= kB8Split4N && K >= kB8Split4MinK) {  // K split over four waves
+        const int nph = b8_phases(NCG, RG, 4, K, I8);
+        if (nph > 0)
+            return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8Split4 : kB8CplF16Split4, 4>(
+                W, sc, x, y, B, N, K, nph, s);
+    }
     if (N < kB8SplitN) {  // K split over the two waves of each row group
         const int nph = b8_phases(NCG, RG, 2, K, I8);
         if (nph > 0)
