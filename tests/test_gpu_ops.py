@@ -765,10 +765,11 @@ def test_gemv_split_k(B, N, K, i8):
                                       (5, 1000, 10624, False)])
 def test_gemv_phased_x(B, N, K, i8):
     """x that does not fit in LDS whole is staged in K phases, W still read
-    once: 2 phases with split K (8 x 14336 fp16), 2 unsplit (8200 rows), 4
-    split (int8 8 x 30720) and 3 unsplit (int8 8192 x 21504: 3 x 7168).  K =
-    10624 = 83 x 128 has no phase count that divides it into whole load
-    steps: batch 5 runs as slices of 4 and 1."""
+    once: 2 phases with K split over four waves (8 x 14336 fp16), 2 unsplit
+    (8200 rows), 5 with K split over four waves (int8 8 x 30720: 5 x 6144)
+    and 3 unsplit (int8 8192 x 21504: 3 x 7168).  K = 10624 = 83 x 128 has no
+    phase count that divides it into whole load steps: batch 5 runs as
+    slices of 4 and 1."""
     r = rng(990 + B + N + K // 128 + i8)
     x = bits(r.standard_normal((B, K)))
     y = torch.empty((B, N), dtype=torch.float16, device="cuda")
