@@ -216,7 +216,13 @@ tecoopsStatus_t tecoopsReshapeAndCacheEx(tecoopsHandle_t handle,
  * drops (api/torch_ext.cpp:99-165): cu_seqlens_q int32 [batch+1] (device) is
  * used when q_seq_lens is NULL, so callers need no host synchronisation;
  * softmax_scale > 0 overrides 1/sqrt(D); causal = 0 disables the mask.
- * workspace NULL uses the handle's scratch; otherwise it must hold
+ * With cu_seqlens_q, output rows past cu_seqlens_q[batch] (rows of no
+ * sequence, e.g. a graph's padding) are written as zeros, as the reference
+ * torch wrapper zeroes its output first (api/torch_ext.cpp:128-132).
+ * workspace NULL uses the handle's scratch for a split-KV decode; on a stream
+ * being captured into a graph that call returns TECOOPS_STATUS_NOT_SUPPORTED
+ * (a later call may free the scratch the graph would keep): pass a workspace
+ * or call tecoopsFlashAttentionNoAlloc there.  A workspace must hold
  * tecoopsGetFlashAttentionWorkspaceSize() bytes for the same batch, heads,
  * head size, max_seqlen_q and max_seqlen_k, and max_seqlen_k must then be > 0
  * (it sizes the split-KV partials). */

@@ -99,6 +99,7 @@ struct FaParams {
     long long page_stride;                      // Hkv * bs * D elements per cache block
     float scale_log2;    // softmax_scale * log2(e)
     int causal;
+    long long total_q;   // rows of q and of the output (q's descriptor)
     // split-KV decode
     float *ws_o;         // [B][Hkv][max_splits][ncols][D]
     float *ws_ml;        // [B][Hkv][max_splits][ncols][2]
@@ -134,6 +135,22 @@ __device__ __forceinline__ void seq_info(const FaParams &p, int b, long long &q_
 // the row.  A negative length counts as 0.
 __device__ __forceinline__ int kv_len(const FaParams &p, int b) {
     return min(max(p.kv_lens[b], 0), p.kv_cap);
+}
+
+// Output rows past cu_seqlens_q[batch] belong to no sequence (padding of a
+// captured graph, say).  With cumulative offsets they are written as zeros,
+// as the reference torch wrapper zeroes its whole output before the call
+// (api/torch_ext.cpp:128-132); the rows of the sequences are all written by
+// the attention kernels, so only this tail needs it.  One workgroup, 16-byte
+// stores; in the usual case the offsets cover every row and nothing is done.
+__device__ __forceinline__ void zero_tail_rows(const FaParams &p, int D) {
+    if (p.cu_q == nullptr) return;
+    const long long end = max(p.cu_q[p.batch], 0);
+    if (end >= p.total_q) return;
+    const long long chunks = static_cast<long long>(p.H) * D / 8;  // per row
+    u32x4 *o = reinterpret_cast<u32x4 *>(p.o);
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    for (long long c = end * chunks + threadIdx.x; c < p.total_q * chunks; c += blockDim.x) o[c] = zero;
 }
 
 // 16-byte K/V load; STREAM selects the non-temporal policy for data read once.
@@ -875,56 +892,73 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
     __syncthreads();  // the next tile of the same workgroup refills the LDS
 }
 
-// Workgroup (b, kv head, head group, query tile) with W waves: wave w serves
-// query head hg*HW + w % HW of the GQA group and query rows
-// [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of TILE keys are double
-// buffered in LDS (one barrier per tile) and attended 32 * NKB keys at a time.
-// W >= 12 asks for 3 waves per SIMD (168 VGPRs); head sizes above 128 with 4
-// waves one (their 4-wave tiles fill the registers), else 2.
-template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
-__global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 && W < 8 ? 1 : 2))
-fa_prefill_kernel(FaParams p) {
-    constexpr int QT = 32 * QSUB * (W / HW);
-    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-    int bx = blockIdx.x;
-    const int ngroups = p.G / HW;
-    const int hg = bx % ngroups;
-    bx /= ngroups;
-    const int kvh = bx % p.Hkv;
-    const int b = bx / p.Hkv;
-    long long q_off;
-    int L;
-    seq_info(p, b, q_off, L);
-    const int tile = gridDim.y - 1 - blockIdx.y;  // heaviest causal tiles first
-    if (tile * QT >= L) return;
-    prefill_tile<T, D, W, HW, QSUB, BSM, TILE>(p, lds, b, kvh, hg, q_off, L, kv_len(p, b),
-                                                tile * QT);
-}
+// A kernel's FaParams argument where it lies, at the start of the kernel
+// argument segment (constant address space): read through this pointer a
+// callee gets the fields with scalar loads, and no copy of the argument is
+// made on the stack.
+// (The host pass only parses device code, and its target has no such
+// address space.)
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef const __attribute__((address_space(4))) FaParams KernargParams;
+#else
+typedef const FaParams KernargParams;
+#endif
 
-// The query tiles from first_tile on, which fa_prefill_kernel's grid (sized
-// from max_seqlen_q, a bound the reference never reads) does not cover: one
-// workgroup per (b, kv head, head group) takes them in turn.  Launched after
-// fa_prefill_kernel whenever a q_len could exceed the grid; with a bound that
-// holds, every workgroup finds no tile and exits.  A kernel of its own, so
-// that fa_prefill_kernel has no loop around its tile (values hoisted out of
-// a loop would stay live across the tile and cost registers).
+// The query tiles of (b, kv head kvh, head group hg) from first_tile on, in
+// turn.  Not inlined: it runs only when max_seqlen_q understates a q length,
+// and its loop keeps values live across tiles that would otherwise push the
+// kernel's single-tile path past its register budget.
 template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
-__global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 && W < 8 ? 1 : 2))
-fa_prefill_rest_kernel(FaParams p, int first_tile) {
+__device__ __attribute__((noinline)) void prefill_rest(const KernargParams *pp, int b, int kvh,
+                                                       int hg, int first_tile) {
     constexpr int QT = 32 * QSUB * (W / HW);
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-    int bx = blockIdx.x;
-    const int ngroups = p.G / HW;
-    const int hg = bx % ngroups;
-    bx /= ngroups;
-    const int kvh = bx % p.Hkv;
-    const int b = bx / p.Hkv;
+    const FaParams p = *pp;
     long long q_off;
     int L;
     seq_info(p, b, q_off, L);
     const int S = kv_len(p, b);
     for (int t = first_tile; t * QT < L; ++t)
         prefill_tile<T, D, W, HW, QSUB, BSM, TILE>(p, lds, b, kvh, hg, q_off, L, S, t * QT);
+}
+
+// Workgroup (b, kv head, head group, query tile) with W waves: wave w serves
+// query head hg*HW + w % HW of the GQA group and query rows
+// [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of TILE keys are double
+// buffered in LDS (one barrier per tile) and attended 32 * NKB keys at a time.
+// W >= 12 asks for 3 waves per SIMD (168 VGPRs); head sizes above 128 with 4
+// waves one (their 4-wave tiles fill the registers), else 2.
+//
+// The grid has one tile row more than max_seqlen_q asks for; that bound is
+// one the reference never reads (flash_attention.cpp:98-99).  Its workgroups
+// are dispatched last and take every query tile past the other rows, in
+// turn.  With a bound that holds there is none, and they exit at once while
+// the tail of the grid drains: a prefill is one launch whatever the bound.
+template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
+__global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 && W < 8 ? 1 : 2))
+fa_prefill_kernel(FaParams p) {
+    constexpr int QT = 32 * QSUB * (W / HW);
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    if (blockIdx.x == 0 && blockIdx.y == 0) zero_tail_rows(p, D);
+    const int ngroups = p.G / HW;
+    const int hg = blockIdx.x % ngroups;
+    const int kvh = (blockIdx.x / ngroups) % p.Hkv;
+    const int b = blockIdx.x / ngroups / p.Hkv;
+    const int rows = gridDim.y - 1;  // tile rows sized from max_seqlen_q
+    long long q_off;
+    int L;
+    seq_info(p, b, q_off, L);
+    const int S = kv_len(p, b);
+    if (blockIdx.y == rows) {
+        if (rows * QT < L)
+            prefill_rest<T, D, W, HW, QSUB, BSM, TILE>(
+                (const KernargParams *)(__builtin_amdgcn_kernarg_segment_ptr()), b, kvh,
+                hg, rows);
+        return;
+    }
+    const int tile = rows - 1 - blockIdx.y;  // heaviest causal tiles first
+    if (tile * QT >= L) return;
+    prefill_tile<T, D, W, HW, QSUB, BSM, TILE>(p, lds, b, kvh, hg, q_off, L, S, tile * QT);
 }
 
 // ----------------------------------------------------------------- decode
@@ -1174,6 +1208,7 @@ __device__ bool decode_item(const FaParams &p, int i, int &b, int &kvh, int &spl
 template <typename T, int D, int BSM>
 __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) fa_decode_kernel(FaParams p) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    if (blockIdx.x == 0 && blockIdx.y == 0) zero_tail_rows(p, D);
     int b, kvh, split, L, S;
     long long q_off;
     if (p.batch <= 64) {
@@ -1322,7 +1357,6 @@ __global__ void __launch_bounds__(256) fa_decode_combine_kernel(FaParams p) {
 struct Plan {
     bool decode;
     int rq, ncols, split_len, max_splits;
-    long long total_q;  // sum of the q lengths (q's descriptor): bounds every q_len
 };
 
 Plan make_plan(int batch, int H, int Hkv, int q_hint, int k_hint) {
@@ -1354,25 +1388,18 @@ size_t workspace_bytes(const Plan &pl, int batch, int Hkv, int D) {
 }
 
 // Prefill over a grid of ceil(q_hint / QT) query tiles per (b, kv head, head
-// group), then, unless q_hint already bounds every q_len (it is at least the
-// total q length), fa_prefill_rest_kernel for the tiles past the grid.
+// group), plus the row that covers any tiles past them.
 template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
 tecoopsStatus_t launch_prefill(const FaParams &p, const Plan &pl, hipStream_t s) {
     constexpr int QT = 32 * QSUB * (W / HW);
     auto *kern = &fa_prefill_kernel<T, D, W, HW, QSUB, BSM, TILE>;
-    auto *rest = &fa_prefill_rest_kernel<T, D, W, HW, QSUB, BSM, TILE>;
     const size_t lds = prefill_lds_bytes<D, TILE, W, HW, QSUB>();
-    if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds) ||
-        !tecoops::reserve_lds(reinterpret_cast<const void *>(rest), lds))
+    if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds))
         return TECOOPS_STATUS_INTERNAL_ERROR;
     const int units = p.batch * p.Hkv * (p.G / HW);
     const int tiles = (pl.rq + QT - 1) / QT;
-    hipLaunchKernelGGL(kern, dim3(units, tiles), dim3(W * 64), lds, s, p);
+    hipLaunchKernelGGL(kern, dim3(units, tiles + 1), dim3(W * 64), lds, s, p);
     TECO_CHECK_LAUNCH("flash_attention prefill");
-    if (static_cast<long long>(tiles) * QT < pl.total_q) {
-        hipLaunchKernelGGL(rest, dim3(units), dim3(W * 64), lds, s, p, tiles);
-        TECO_CHECK_LAUNCH("flash_attention prefill (rest)");
-    }
     return TECOOPS_STATUS_SUCCESS;
 }
 
@@ -1514,11 +1541,12 @@ struct FaCall {
 
 // Argument checks of reference flash_attention.cpp:44-69, extended to bf16 and
 // to the shape facts the kernels rely on; fills everything but the split-KV
-// workspace.  max_seqlen_q / max_seqlen_k are launch-shape hints only: values
-// <= 0 are accepted (the reference never reads them) and replaced by bounds
-// the host knows, the mean q length (sum(q) / batch from q's descriptor) and
-// the block-table width * block_size.  fixed_k_hint keeps max_seqlen_k as
-// given, for a caller workspace sized by tecoopsGetFlashAttentionWorkspaceSize.
+// workspace.  max_seqlen_q / max_seqlen_k are launch-shape hints only: any
+// value is accepted (the reference never reads them).  The q hint is raised to
+// the mean q length (sum(q) / batch from q's descriptor) and the k hint
+// capped by the block-table width * block_size, or taken as that width when
+// <= 0.  fixed_hints keeps both as given (a q hint <= 0 becoming the mean),
+// for a caller workspace sized by tecoopsGetFlashAttentionWorkspaceSize.
 tecoopsStatus_t fa_prepare(tecoopsHandle_t handle, int max_seqlen_q, int max_seqlen_k,
                            const int *q_seq_lens, const int *cu_seqlens_q, const int *kv_seq_lens,
                            const tecoopsTensorDescriptor_t btDesc, const void *blockTable,
@@ -1526,7 +1554,7 @@ tecoopsStatus_t fa_prepare(tecoopsHandle_t handle, int max_seqlen_q, int max_seq
                            const tecoopsTensorDescriptor_t kDesc, const void *kCache,
                            const tecoopsTensorDescriptor_t vDesc, const void *vCache,
                            const tecoopsTensorDescriptor_t oDesc, void *oData, float softmax_scale,
-                           int causal, bool fixed_k_hint, FaCall &c) {
+                           int causal, bool fixed_hints, FaCall &c) {
     if (handle == nullptr) return TECOOPS_STATUS_NOT_INITIALIZED;
     if (!btDesc || !qDesc || !kDesc || !vDesc || !oDesc) return TECOOPS_STATUS_BAD_PARAM;
     if (!blockTable || !qData || !kCache || !vCache || !oData || !kv_seq_lens)
@@ -1557,7 +1585,7 @@ tecoopsStatus_t fa_prepare(tecoopsHandle_t handle, int max_seqlen_q, int max_seq
                    "num_heads must be a multiple of num_kv_heads");
     TECO_RETURN_IF(bs <= 0 || num_blocks <= 0 || batch <= 0 || total_q < 0 || bt_cols < 0,
                    TECOOPS_STATUS_BAD_PARAM, "empty cache or batch");
-    TECO_RETURN_IF(fixed_k_hint && max_seqlen_k <= 0, TECOOPS_STATUS_BAD_PARAM,
+    TECO_RETURN_IF(fixed_hints && max_seqlen_k <= 0, TECOOPS_STATUS_BAD_PARAM,
                    "flash_attention: a caller workspace needs the max_seqlen_k it was sized for");
     TECO_RETURN_IF(!is_packed_rowmajor(qDesc) || !is_packed_rowmajor(oDesc) ||
                    !is_packed_rowmajor(kDesc) || !is_packed_rowmajor(vDesc) ||
@@ -1592,11 +1620,18 @@ tecoopsStatus_t fa_prepare(tecoopsHandle_t handle, int max_seqlen_q, int max_seq
     p.scale_log2 = scale * 1.4426950408889634f;
     p.causal = causal != 0;
 
-    const int q_hint = max_seqlen_q > 0 ? max_seqlen_q : std::max(1, (total_q + batch - 1) / batch);
+    // The q bound routes the call (decode or prefill) and sizes the prefill
+    // grid.  It is raised to the mean q length, which the host knows: a bound
+    // that is too small (the reference never reads it) would otherwise send a
+    // prefill down the decode route, correct but many times slower.  A caller
+    // workspace was sized for the bounds as given, so they are kept then.
+    const int q_mean = std::max(1, (total_q + batch - 1) / batch);
+    const int q_hint = fixed_hints ? (max_seqlen_q > 0 ? max_seqlen_q : q_mean)
+                                    : std::max(max_seqlen_q, q_mean);
     int k_hint = max_seqlen_k;
-    if (!fixed_k_hint) k_hint = max_seqlen_k > 0 ? std::min(max_seqlen_k, p.kv_cap) : p.kv_cap;
+    if (!fixed_hints) k_hint = max_seqlen_k > 0 ? std::min(max_seqlen_k, p.kv_cap) : p.kv_cap;
     c.pl = make_plan(batch, H, Hkv, q_hint, k_hint);
-    c.pl.total_q = total_q;
+    p.total_q = total_q;
     if (c.pl.decode) {
         p.rq = c.pl.rq;
         p.ncols = c.pl.ncols;
@@ -1664,7 +1699,9 @@ extern "C" tecoopsStatus_t tecoopsFlashAttentionEx(
                                     workspace != nullptr, c);
     if (st != TECOOPS_STATUS_SUCCESS) return st;
     void *ws = workspace;
-    if (c.pl.decode && ws == nullptr) {
+    // With one split per sequence the decode kernel writes the output rows
+    // itself and reads no partials: no scratch is needed then.
+    if (c.pl.decode && c.pl.max_splits > 1 && ws == nullptr) {
         st = tecoops::handle_scratch(handle, fa_workspace_bytes(c), &ws);
         if (st != TECOOPS_STATUS_SUCCESS) return st;
     }

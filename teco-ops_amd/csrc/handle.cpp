@@ -212,6 +212,21 @@ bool reserve_lds(const void *kernel, size_t bytes) {
 }
 
 tecoopsStatus_t handle_scratch(tecoopsHandle_t handle, size_t bytes, void **out) {
+    // A graph captured from this stream would keep the slot's address, and a
+    // later call may free the slot (a larger plan grows it, a ninth stream
+    // takes it over), leaving the graph writing freed memory.  Under capture
+    // the caller passes a workspace or uses the allocation-free entry point.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(handle->stream, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        cs = hipStreamCaptureStatusNone;
+    }
+    if (cs != hipStreamCaptureStatusNone) {
+        TECO_ERROR("the handle's split-KV scratch cannot be used while its stream is captured: "
+                   "pass a workspace (tecoopsFlashAttentionEx) or call "
+                   "tecoopsFlashAttentionNoAlloc");
+        return TECOOPS_STATUS_NOT_SUPPORTED;
+    }
     if (bytes == 0) bytes = 256;
     ScratchSlot *slot = nullptr;
     for (ScratchSlot &sl : handle->scratch)

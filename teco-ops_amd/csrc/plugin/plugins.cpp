@@ -19,7 +19,8 @@
 //   * flash attention passes the block table's real shape and differences
 //     cu_seqlens_q on the device (the reference leaves bt_shape empty and
 //     passes cumulative offsets where per-batch lengths are expected,
-//     plugin_flash_attention.cc:79, :98, :108);
+//     plugin_flash_attention.cc:79, :98, :108); on a stream being captured
+//     into a graph it calls the allocation-free entry point;
 //   * causal_conv1d treats the stride attributes' default 0 as "packed"
 //     (dim for x / out rows, (width-1)*dim for conv_state entries), and
 //     copies the updated state on the engine stream instead of a blocking
@@ -332,21 +333,39 @@ class PluginFlashAttentionImpl : public AbstractPluginOp {
         ctx->GetAttr("max_seqlen_k", max_k);
         ctx->GetAttr("softmax_scale", scale);
         ctx->GetAttr("causal", causal);
-        // Unset bounds fall back to what the shapes guarantee.
-        if (max_q <= 0) max_q = qs[0];
-        if (max_k <= 0) max_k = static_cast<int64_t>(bts[1]) * ks[2];
+        // Unset bounds (<= 0) go through as they are: the library derives them
+        // from the shapes (the mean q length, the block-table width * block
+        // size).  The reference sets neither.
         require(max_q <= INT32_MAX && max_k <= INT32_MAX, "max_seqlen out of range");
         const tecoopsDataType_t t = ctx->GetInputDataType("q");
         Desc bt_d(TECOOPS_DATA_INT32, bts), q_d(t, qs), k_d(t, ks), v_d(t, vs), o_d(t, qs);
-        check(tecoopsFlashAttentionEx(handle_.bind(ctx->GetStream()), static_cast<int>(max_q),
-                                      static_cast<int>(max_k), nullptr,
-                                      static_cast<const int *>(ctx->GetInputDataPtr("cu_seqlens_q")),
-                                      static_cast<const int *>(ctx->GetInputDataPtr("seqused_k")), bt_d,
-                                      ctx->GetInputDataPtr("block_table"), q_d, ctx->GetInputDataPtr("q"),
-                                      k_d, ctx->GetInputDataPtr("k_cache"), v_d,
-                                      ctx->GetInputDataPtr("v_cache"), o_d, ctx->GetOutputDataPtr(0),
-                                      static_cast<float>(scale), static_cast<int>(causal != 0), nullptr),
-              "plugin_flash_attention");
+        hipStream_t stream = ctx->GetStream();
+        tecoopsHandle_t h = handle_.bind(stream);
+        const auto *cu = static_cast<const int *>(ctx->GetInputDataPtr("cu_seqlens_q"));
+        const auto *kv = static_cast<const int *>(ctx->GetInputDataPtr("seqused_k"));
+        // An engine capturing its stream into a graph gets the allocation-free
+        // entry point: the handle's split-KV scratch can be freed by a later
+        // call while the graph still holds its address.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+            (void)hipGetLastError();
+            cs = hipStreamCaptureStatusNone;
+        }
+        if (cs != hipStreamCaptureStatusNone)
+            check(tecoopsFlashAttentionNoAlloc(
+                      h, static_cast<int>(max_q), static_cast<int>(max_k), nullptr, cu, kv, bt_d,
+                      ctx->GetInputDataPtr("block_table"), q_d, ctx->GetInputDataPtr("q"), k_d,
+                      ctx->GetInputDataPtr("k_cache"), v_d, ctx->GetInputDataPtr("v_cache"), o_d,
+                      ctx->GetOutputDataPtr(0), static_cast<float>(scale), static_cast<int>(causal != 0)),
+                  "plugin_flash_attention");
+        else
+            check(tecoopsFlashAttentionEx(
+                      h, static_cast<int>(max_q), static_cast<int>(max_k), nullptr, cu, kv, bt_d,
+                      ctx->GetInputDataPtr("block_table"), q_d, ctx->GetInputDataPtr("q"), k_d,
+                      ctx->GetInputDataPtr("k_cache"), v_d, ctx->GetInputDataPtr("v_cache"), o_d,
+                      ctx->GetOutputDataPtr(0), static_cast<float>(scale), static_cast<int>(causal != 0),
+                      nullptr),
+                  "plugin_flash_attention");
     }
 
  private:

@@ -157,13 +157,16 @@ void flash_attn_varlen_func(const Tensor &q, const Tensor &k, const Tensor &v,
     // where the handle's own scratch (hipMalloc on a stream's first use) could
     // not be allocated.  The launch hints are the ones the library derives
     // without a workspace (mean q length; max_seqlen_k capped by the
-    // block-table width * block size), so the plan and results are unchanged.
+    // block-table width * block size), so the plan and results are unchanged:
+    // max_seqlen_q raised to the mean q length, max_seqlen_k capped by (or,
+    // when <= 0, taken as) the block-table width * block size.
     int q_hint = static_cast<int>(max_seqlen_q), k_hint = static_cast<int>(max_seqlen_k);
     Tensor ws;
     if (q.dim() == 3 && k.dim() == 4 && block_table.dim() == 2 && block_table.size(0) > 0) {
         const int64_t batch = block_table.size(0);
         const int64_t cap = std::min<int64_t>(block_table.size(1) * k.size(2), 0x7fffffff);
-        if (q_hint <= 0) q_hint = static_cast<int>(std::max<int64_t>(1, (q.size(0) + batch - 1) / batch));
+        const int64_t q_mean = std::max<int64_t>(1, (q.size(0) + batch - 1) / batch);
+        q_hint = static_cast<int>(std::min<int64_t>(std::max(max_seqlen_q, q_mean), 0x7fffffff));
         k_hint = static_cast<int>(max_seqlen_k > 0 ? std::min<int64_t>(max_seqlen_k, cap) : cap);
         size_t bytes = 0;
         if (k_hint > 0 &&

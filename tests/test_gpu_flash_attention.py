@@ -578,3 +578,92 @@ def test_decode_from_two_threads():
     for i, (q, kc, vc, bt, kv) in enumerate(jobs):
         ref = orc.flash_attention(q, kc, vc, bt, [1] * 32, kv, dtype=orc.BF16)
         assert_close(outs[i], ref, what=f"thread {i}")
+
+
+@pytest.mark.parametrize("H,Hkv", [(40, 8), (64, 8)])
+def test_query_heads_past_32(H, Hkv):
+    """Query heads 32 and up are attended like any other.  The reference
+    kernel stops at head 32 (one head per SPE of 32: `tid >= MIN(spe_num,
+    local_head_num)` returns, teco/ual/kernel/flash_attention/
+    flash_attention.scpp:181-183) and its torch wrapper zeroes `out` first
+    (api/torch_ext.cpp:128-132), so there heads 32.. come back as zeros; here
+    they match the oracle.  Prefill, chunked and decode shapes; GQA groups of
+    5 (one head per wave group) and 8."""
+    for q_lens, kv in (([700, 130], [700, 900]), ([1] * 9, [40, 900, 5000, 2100, 17, 3000, 1, 64, 513])):
+        q, kc, vc, bt = make_inputs(40 + H, H, Hkv, 128, 16, q_lens, kv, dtype=orc.BF16,
+                                    dist="normal")
+        got = run_gpu(q, kc, vc, bt, q_lens, kv, orc.BF16)
+        ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=orc.BF16)
+        assert np.abs(ref[:, 32:]).max() > 0.1, "the upper heads carry non-trivial output"
+        assert_close(got[:, 32:], ref[:, 32:], what=f"heads 32..{H - 1} of H={H}, q_lens {q_lens[:3]}")
+        assert_close(got, ref, what=f"all heads of H={H}")
+
+
+@pytest.mark.parametrize("front", ["tecoops", "torch.ops"])
+@pytest.mark.parametrize("kind", ["prefill", "decode"])
+def test_rows_past_cu_seqlens_are_zero(front, kind):
+    """q and out hold 5 rows more than cu_seqlens_q[batch] (padding, as a
+    captured graph's fixed-size buffers have): those output rows come back as
+    zeros, as the reference torch wrapper zeroes its whole output before the
+    call (api/torch_ext.cpp:128-132); every row of a sequence matches the
+    oracle.  The output starts filled with NaN."""
+    q_lens, kv = ([300, 77, 129], [300, 500, 129]) if kind == "prefill" else ([1] * 12, list(range(100, 6100, 500)))
+    q, kc, vc, bt = make_inputs(61, 16, 4, 128, 16, q_lens, kv, dtype=orc.BF16)
+    pad = 5
+    qp = np.concatenate([q, np.full((pad,) + q.shape[1:], 0x3f80, q.dtype)])  # padding rows hold 1.0
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    out = torch.full(qp.shape, float("nan"), dtype=torch.bfloat16, device="cuda")
+    args = (dev(qp, orc.BF16), dev(kc, orc.BF16), dev(vc, orc.BF16), max(q_lens), dev(cu), max(kv),
+            None, dev(np.array(kv, np.int32)), 1.0 / math.sqrt(128), True, None, dev(bt), False, out)
+    if front == "tecoops":
+        tecoops.flash_attn_varlen_func(*args)
+    else:
+        torch.ops.tecoops.flash_attn_varlen_func(*args)
+    torch.cuda.synchronize()
+    got = as_f32(out, orc.BF16)
+    assert (got[sum(q_lens):] == 0).all(), "rows past cu_seqlens_q[batch] must be zero"
+    ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=orc.BF16)
+    assert_close(got[:sum(q_lens)], ref, what=f"{kind} rows of the sequences ({front})")
+
+
+def test_handle_scratch_refused_under_capture():
+    """A split-KV decode without a workspace takes the handle's scratch, which
+    a later call may free; on a stream being captured into a graph the call
+    is refused before anything is enqueued (NOT_SUPPORTED, naming the
+    alternatives).  A single-split decode needs no scratch and is captured
+    and replayed; the same decode then runs eagerly and matches the oracle."""
+    from tecoops import _lib
+    kv_long = [3000, 5000, 4100, 2500]
+    q, kc, vc, bt = make_inputs(62, 16, 4, 128, 16, [1] * 4, kv_long, dtype=orc.BF16)
+    cu = dev(np.arange(5, dtype=np.int32))
+    args = lambda out, kvd, mk: (dev(q, orc.BF16), dev(kc, orc.BF16), dev(vc, orc.BF16), 1, cu, mk,
+                                 None, kvd, 1.0 / math.sqrt(128), True, None, dev(bt), False, out)
+    out = torch.zeros(q.shape, dtype=torch.bfloat16, device="cuda")
+    kvd = dev(np.array(kv_long, np.int32))
+    a = args(out, kvd, max(kv_long))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(_lib.TecoopsError) as ei:
+        with torch.cuda.graph(graph):
+            tecoops.flash_attn_varlen_func(*a)
+    assert ei.value.status == _lib.NOT_SUPPORTED, str(ei.value)
+    torch.cuda.synchronize()
+    # single split (every kv length within 512 keys): no scratch, capture works
+    kv_short = [300, 17, 511, 1]
+    kvs = dev(np.array(kv_short, np.int32))
+    out2 = torch.zeros(q.shape, dtype=torch.bfloat16, device="cuda")
+    a2 = args(out2, kvs, max(kv_short))
+    tecoops.flash_attn_varlen_func(*a2)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        tecoops.flash_attn_varlen_func(*a2)
+    out2.zero_()
+    g2.replay()
+    torch.cuda.synchronize()
+    ref2 = orc.flash_attention(q, kc, vc, bt, [1] * 4, kv_short, dtype=orc.BF16)
+    assert_close(as_f32(out2, orc.BF16), ref2, what="single-split decode replayed from a graph")
+    tecoops.flash_attn_varlen_func(*a)
+    torch.cuda.synchronize()
+    ref = orc.flash_attention(q, kc, vc, bt, [1] * 4, kv_long, dtype=orc.BF16)
+    assert_close(as_f32(out, orc.BF16), ref, what="split-KV decode after the refused capture")

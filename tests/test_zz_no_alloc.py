@@ -4,7 +4,8 @@ live in a static device array), against tecoopsFlashAttentionEx on the same
 inputs, through the C ABI.  Both launch the same kernels with the same plan,
 so the outputs must be bit-identical.  Two calls in a row, the second with a
 smaller batch, then a prefill call and a decode whose plan needs more than
-the static array (rejected)."""
+the static array (rejected), and a decode captured into a graph and
+replayed."""
 import ctypes
 import math
 
@@ -87,3 +88,50 @@ def test_no_alloc_prefill_and_limit():
     kl = torch.ones((B,), dtype=torch.int32, device="cuda")
     st, _ = call("tecoopsFlashAttentionNoAlloc", q, kc, kc, bt, cu, kl, 1, 1 << 20)
     assert st == _lib.BAD_PARAM
+
+
+def test_no_alloc_graph_capture_replays():
+    """The entry point's use case: a split-KV decode captured into a graph on
+    a torch stream after one eager call (the first call looks up the static
+    array's device address and raises the kernels' LDS limit), then replayed
+    twice with new q written in between; each replay is bit-identical to the
+    Ex entry point run eagerly on the same inputs."""
+    rng = np.random.default_rng(9)
+    q, kc, vc, bt, cu, kl = make(16, 32, 8, 128, 16, [1] * 16, rng.integers(600, 6000, 16).tolist(), 4)
+    mk = int(kl.max())
+    out = torch.zeros(q.shape, dtype=torch.bfloat16, device="cuda")
+    code = _lib.DATA_BFLOAT16
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    scale = ctypes.c_float(1.0 / math.sqrt(q.shape[2]))
+    with tecoops._Desc(bt, _lib.DATA_INT32) as btd, tecoops._Desc(q, code) as qd, \
+            tecoops._Desc(kc, code) as kd, tecoops._Desc(vc, code) as vd, \
+            tecoops._Desc(out, code) as od:
+        def enqueue():
+            return _lib.lib().tecoopsFlashAttentionNoAlloc(
+                tecoops._handle(q.device), 1, mk, None, p(cu), p(kl), btd, p(bt), qd, p(q), kd, p(kc),
+                vd, p(vc), od, p(out), scale, 1)
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            assert enqueue() == _lib.SUCCESS
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        status = []
+        with torch.cuda.graph(graph):
+            status.append(enqueue())
+        assert status == [_lib.SUCCESS]
+        g = torch.Generator(device="cuda").manual_seed(17)
+        prev = None
+        for rep in range(2):
+            q.copy_(torch.randn(q.shape, generator=g, device="cuda").to(torch.bfloat16))
+            out.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            st, ref = call("tecoopsFlashAttentionEx", q, kc, vc, bt, cu, kl, 1, mk)
+            assert st == _lib.SUCCESS
+            assert same(out, ref), f"replay {rep} differs from the Ex entry point"
+            if prev is not None:
+                assert not same(out, prev), "the second replay saw the new q"
+            prev = out.clone()
