@@ -35,7 +35,9 @@ fraction of the MI355X peak.  `roofline` is the dominant kernel's (by time).
 `cpu_baseline` times the CPU oracle (the reference algorithms restated in C)
 on the host cores on a bounded sample of the FA prefill config, with a
 single-thread figure beside it; `cpu_ops` times the oracle on every other op
-at its full config.  Both are reported baselines, not targets.
+at its full config, on all host cores and on one thread (the reference
+harness's own CPU loops are single-threaded).  Both are reported baselines,
+not targets.
 """
 import argparse
 import json
@@ -359,13 +361,33 @@ def cpu_single_thread(budget_s=5.0):
 
 
 def cpu_ops(threads):
-    """Times the CPU oracle on every other op at its full BASELINE config
-    (median of 3 runs; FA decode once), on `threads` host threads.  A
-    reported baseline beside the GPU figures, not a target."""
+    """Times the CPU oracle on every other op at its full BASELINE config, on
+    all `threads` host threads (median of 3 runs; FA decode once) and on one
+    thread (one run each), the way the reference harness's cpuCompute loops
+    run (single-threaded: test/zoo/teco/rms_norm/rms_norm.cpp:195-234,
+    reshape_and_cache/reshape_and_cache.cpp:116-148).  A reported baseline
+    beside the GPU figures, not a target."""
     from oracle import oracle as orc
     if threads > 0:
         orc.set_threads(threads)
     used = orc.get_threads()
+    all_cores = _cpu_ops_once(orc, runs=3)
+    orc.set_threads(1)
+    try:
+        one = _cpu_ops_once(orc, runs=1)
+    finally:
+        orc.set_threads(used)
+    return {"cores": used, "unit": "ms", "kind": "port",
+            "sample": "full BASELINE config of each op; all cores: median of 3 runs (fa_decode 1 "
+                      "run); one thread: 1 run",
+            "ms": {k: round(v, 3) for k, v in all_cores.items()},
+            "ms_1thread": {k: round(v, 3) for k, v in one.items()}}
+
+
+def _cpu_ops_once(orc, runs):
+    """{op: ms} of the oracle on every op but FA prefill at its full config,
+    on the oracle's current thread count; median of `runs` runs (FA decode
+    always one)."""
     rng = np.random.default_rng(11)
 
     # Inputs repeat a 1 Mi-element pool of seeded values, uniform on (-1, 1)
@@ -380,7 +402,7 @@ def cpu_ops(threads):
             return np.resize(pools[dt], shape)
         return orc.from_float(np.resize(pool, shape) * np.float32(scale), dt)
 
-    def timed(fn, runs=3):
+    def timed(fn, runs=runs):
         ts = []
         for _ in range(runs):
             t0 = time.perf_counter()
@@ -426,9 +448,7 @@ def cpu_ops(threads):
     res["fa_decode"] = timed(lambda: orc.flash_attention(dq, dk, dv, bt, np.ones(64, np.int32),
                                                          lens.astype(np.int32), dtype=orc.BF16),
                              runs=1)
-    return {"cores": used, "unit": "ms", "kind": "port",
-            "sample": "full BASELINE config of each op (median of 3 runs; fa_decode 1 run)",
-            "ms": {k: round(v, 3) for k, v in res.items()}}
+    return res
 
 
 def cpu_model():
