@@ -40,6 +40,7 @@ SOURCES = [
     "causal_conv1d.hip",
     "gemv.hip",
     "flash_attention.hip",
+    "fa_noalloc.hip",
 ]
 
 ARCH = os.environ.get("TECOOPS_OFFLOAD_ARCH", "gfx950")

@@ -97,8 +97,12 @@ inline unsigned ceil_div(long long a, long long b) {
 constexpr size_t kLdsMax = 160 * 1024;
 constexpr size_t kLdsDefault = 64 * 1024;
 
-// Raises a kernel's dynamic-LDS limit to `bytes` (above kLdsDefault) once per
-// process and kernel address; false (with the HIP error cleared) if refused.
+// Sets a kernel's dynamic-LDS attribute to `bytes` (above kLdsDefault) when
+// that is more than any size set for it before; false (with the HIP error
+// cleared) above kLdsMax or if refused.  HIP documents that AMD devices may
+// ignore this attribute (hipFuncAttribute in hip_runtime_api.h); the launch
+// itself then checks the dynamic LDS against the workgroup limit, kLdsMax on
+// gfx950.  It is set anyway, for a runtime that does enforce it.
 bool reserve_lds(const void *kernel, size_t bytes);
 
 // Compute units of the current device, queried once per device (256 on

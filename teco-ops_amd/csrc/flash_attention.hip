@@ -44,14 +44,17 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
-#include <mutex>
 
 #include "common.h"
 #include "device.h"
+#include "flash_attention.h"
 
 namespace {
 
 using namespace tecoops::dev;
+using tecoops::fa::FaCall;
+using tecoops::fa::FaParams;
+using tecoops::fa::Plan;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -84,27 +87,6 @@ template <> struct Mma<f16> {
 
 constexpr float kNegInf = -INFINITY;
 
-struct FaParams {
-    const uint16_t *q;
-    const uint16_t *kc;
-    const uint16_t *vc;
-    uint16_t *o;
-    const int *bt;
-    long long bt_stride;
-    const int *q_lens;   // per-sequence q lengths, or NULL
-    const int *cu_q;     // cumulative q offsets [batch+1], used when q_lens is NULL
-    const int *kv_lens;
-    int batch, H, Hkv, G, bs, lbs, num_blocks;  // lbs = log2(bs) when bs is a power of 2
-    int kv_cap;          // block-table width * block_size: kv lengths are clamped to it
-    long long page_stride;                      // Hkv * bs * D elements per cache block
-    float scale_log2;    // softmax_scale * log2(e)
-    int causal;
-    long long total_q;   // rows of q and of the output (q's descriptor)
-    // split-KV decode
-    float *ws_o;         // [B][Hkv][max_splits][ncols][D]
-    float *ws_ml;        // [B][Hkv][max_splits][ncols][2]
-    int split_len, max_splits, rq, ncols;
-};
 
 // P values are computed against a running max that is only raised when a
 // tile's max exceeds it by more than this (log2 domain), so that the O / l
@@ -1350,14 +1332,6 @@ __global__ void __launch_bounds__(256) fa_decode_combine_kernel(FaParams p) {
 
 // ------------------------------------------------------------------- host
 
-// Launch shape.  rq is the host's bound on q_len (routing and grid height),
-// split_len / max_splits the split-KV plan from its bound on kv_len.  Neither
-// bound changes the output (the kernels also cover longer sequences), only
-// the speed.
-struct Plan {
-    bool decode;
-    int rq, ncols, split_len, max_splits;
-};
 
 Plan make_plan(int batch, int H, int Hkv, int q_hint, int k_hint) {
     Plan pl{};
@@ -1531,13 +1505,6 @@ bool is_packed_rowmajor(const tecoopsTensorStruct *d) {
     return true;
 }
 
-// A validated call: kernel parameters, launch shape and element type.
-struct FaCall {
-    FaParams p;
-    Plan pl;
-    int D;
-    bool bf16;
-};
 
 // Argument checks of reference flash_attention.cpp:44-69, extended to bf16 and
 // to the shape facts the kernels rely on; fills everything but the split-KV
@@ -1664,6 +1631,29 @@ tecoopsStatus_t fa_launch(hipStream_t s, FaCall &c, void *ws) {
 
 }  // namespace
 
+namespace tecoops {
+namespace fa {
+
+tecoopsStatus_t prepare(tecoopsHandle_t handle, int max_seqlen_q, int max_seqlen_k,
+                        const int *q_seq_lens, const int *cu_seqlens_q, const int *kv_seq_lens,
+                        const tecoopsTensorDescriptor_t btDesc, const void *blockTable,
+                        const tecoopsTensorDescriptor_t qDesc, const void *qData,
+                        const tecoopsTensorDescriptor_t kDesc, const void *kCache,
+                        const tecoopsTensorDescriptor_t vDesc, const void *vCache,
+                        const tecoopsTensorDescriptor_t oDesc, void *oData, float softmax_scale,
+                        int causal, bool fixed_hints, FaCall &c) {
+    return fa_prepare(handle, max_seqlen_q, max_seqlen_k, q_seq_lens, cu_seqlens_q, kv_seq_lens,
+                      btDesc, blockTable, qDesc, qData, kDesc, kCache, vDesc, vCache, oDesc, oData,
+                      softmax_scale, causal, fixed_hints, c);
+}
+
+size_t workspace_bytes(const FaCall &c) { return fa_workspace_bytes(c); }
+
+tecoopsStatus_t launch(hipStream_t s, FaCall &c, void *ws) { return fa_launch(s, c, ws); }
+
+}  // namespace fa
+}  // namespace tecoops
+
 extern "C" tecoopsStatus_t tecoopsGetFlashAttentionWorkspaceSize(int batch, int num_heads,
                                                                  int head_size, int max_seqlen_q,
                                                                  int max_seqlen_k, size_t *bytes) {
@@ -1728,67 +1718,3 @@ extern "C" tecoopsStatus_t tecoopsFlashAttention(
                                    -1.0f, 1, nullptr);
 }
 
-// ------------------------------------------------ allocation-free entry point
-
-namespace {
-
-// Split-KV partials of tecoopsFlashAttentionNoAlloc: a static device array.
-// Each GPU the library runs on holds its own copy, at its own address, until
-// the process ends.  Every NoAlloc call on a GPU shares that GPU's copy.
-constexpr size_t kStaticScratchBytes = size_t(64) << 20;
-static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
-
-// Device address of this GPU's copy of `scratch`, looked up once per device
-// with that device current.  In host code the array's name is only a
-// host-side stand-in; kernels must get this address instead.
-tecoopsStatus_t static_scratch(void **out) {
-    constexpr int kMaxDevices = 64;
-    static std::mutex mu;
-    static void *addr[kMaxDevices];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-        (void)hipGetLastError();
-        return TECOOPS_STATUS_INTERNAL_ERROR;
-    }
-    std::lock_guard<std::mutex> lock(mu);
-    if (addr[dev] == nullptr) {
-        void *p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
-            (void)hipGetLastError();
-            TECO_ERROR("flash_attention: cannot get the static scratch address on device %d", dev);
-            return TECOOPS_STATUS_INTERNAL_ERROR;
-        }
-        addr[dev] = p;
-    }
-    *out = addr[dev];
-    return TECOOPS_STATUS_SUCCESS;
-}
-
-}  // namespace
-
-extern "C" tecoopsStatus_t tecoopsFlashAttentionNoAlloc(
-    tecoopsHandle_t handle, int max_seqlen_q, int max_seqlen_k, const int *q_seq_lens,
-    const int *cu_seqlens_q, const int *kv_seq_lens, const tecoopsTensorDescriptor_t btDesc,
-    const void *blockTable, const tecoopsTensorDescriptor_t qDesc, const void *qData,
-    const tecoopsTensorDescriptor_t kDesc, const void *kCache,
-    const tecoopsTensorDescriptor_t vDesc, const void *vCache,
-    const tecoopsTensorDescriptor_t oDesc, void *oData, float softmax_scale, int causal) {
-    FaCall c;
-    tecoopsStatus_t st = fa_prepare(handle, max_seqlen_q, max_seqlen_k, q_seq_lens, cu_seqlens_q,
-                                    kv_seq_lens, btDesc, blockTable, qDesc, qData, kDesc, kCache,
-                                    vDesc, vCache, oDesc, oData, softmax_scale, causal, false, c);
-    if (st != TECOOPS_STATUS_SUCCESS) return st;
-    void *ws = nullptr;
-    if (c.pl.decode) {
-        const size_t need = fa_workspace_bytes(c);
-        TECO_RETURN_IF(need > kStaticScratchBytes, TECOOPS_STATUS_BAD_PARAM,
-                       "tecoopsFlashAttentionNoAlloc: split-KV decode needs %zu bytes of scratch, "
-                       "more than the static %zu (use tecoopsFlashAttentionEx)",
-                       need, kStaticScratchBytes);
-        st = static_scratch(&ws);
-        if (st != TECOOPS_STATUS_SUCCESS) return st;
-    }
-    // Every partial the combine kernel reads is written by the same call's
-    // decode kernel first, so the scratch needs no clearing.
-    return fa_launch(handle->stream, c, ws);
-}

@@ -14,8 +14,8 @@
 //     matrix-core path ("MFMA path" below), in slices of 16 columns.
 //   * 1-2 and all other shapes: the VALU path, which streams W fastest when
 //     there is little math per byte.  A workgroup of 4 waves owns 4*R
-//     consecutive output rows and stages x ([B, K], at most 64 KiB) in
-//     LDS; x (and the int8 scales) are loaded before W, so that waiting for
+//     consecutive output rows and stages x ([B, K], up to the workgroup's
+//     160 KiB) in LDS; x (and the int8 scales) are loaded before W, so that waiting for
 //     them leaves W in flight.  Each wave streams R rows of W with 16-byte
 //     loads, lane-interleaved
 //     along K so that every load instruction reads a contiguous 1 KiB run of
@@ -500,7 +500,9 @@ template <> struct Mma4<bf16> {
     }
 };
 
-// Staged x is at most 64 KiB: 4096 16-byte chunks.
+// x chunks (16 bytes) a workgroup of the 4x4x4 path loads into registers
+// ahead of its first W loads (64 KiB, the whole x of batch 8 at K = 4096); a
+// larger staged x copies the chunks past these straight to LDS.
 constexpr int kMaxXChunks = 4096;
 
 // LDS element offset of the 16-byte chunk c of staged x row `row`.
@@ -755,8 +757,8 @@ gemv_scalar_kernel(const void *__restrict__ Wv, const uint16_t *__restrict__ sca
     }
 }
 
-// x staged in LDS may fill a workgroup's whole LDS (the kernels' limit is
-// raised above the default 64 KiB when it does).
+// x staged in LDS may fill a workgroup's whole LDS (reserve_lds sets the
+// kernels' attribute above the default 64 KiB when it does).
 constexpr long long kMaxLdsBytes = static_cast<long long>(tecoops::kLdsMax);
 
 // Matrix-core path: smallest batch that takes it, row tiles of 16 per
@@ -783,8 +785,8 @@ constexpr int kR16 = 1, kCpl16 = 8;
 constexpr int kRI8 = 2, kCplI8 = 4;
 
 // 4x4x4 path: groups of 4 rows per wave and load steps in flight per lane,
-// for fp16 / int8 W.  x fills at most 64 KiB of LDS and is staged once per
-// workgroup, so workgroups are large (b8_waves picks their size).  Measured
+// for fp16 / int8 W.  x is staged in LDS once per workgroup, so workgroups
+// are large (b8_waves picks their size).  Measured
 // at batch 8 on [14336, 4096], same box: int8 with 1, 2, 3, 4, 8 and 16
 // steps in flight took 16.5, 12.6, 13.1, 14.9, 15.9 and 16.3 us (2 row
 // groups per wave: 15.0-15.6 us); fp16 with 2, 4, 6, 8, 10, 12 and 16 took

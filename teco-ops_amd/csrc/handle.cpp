@@ -190,24 +190,37 @@ tecoopsStatus_t tecoopsMorton3DInvert(tecoopsHandle_t handle, const int *indices
 
 namespace tecoops {
 
-// The kernels already raised are kept in a fixed table (no heap allocation, so
-// the allocation-free entry points can use it too); past its capacity the
-// attribute is simply set again on every launch.
+// The largest size set for each kernel so far is kept in a fixed table (no
+// heap allocation, so the allocation-free entry points can use it too): the
+// attribute is set again only when a launch needs more than that (the GEMV
+// kernels' LDS grows with K), and past the table's capacity on every launch.
 bool reserve_lds(const void *kernel, size_t bytes) {
     static std::mutex mu;
-    static const void *done[256];
-    static int ndone = 0;
+    static const void *kern[256];
+    static size_t size[256];
+    static int n = 0;
     if (bytes <= kLdsDefault) return true;
+    if (bytes > kLdsMax) {
+        TECO_ERROR("a kernel asks for %zu bytes of LDS, more than the %zu a workgroup can hold",
+                   bytes, kLdsMax);
+        return false;
+    }
     std::lock_guard<std::mutex> lock(mu);
-    for (int i = 0; i < ndone; ++i)
-        if (done[i] == kernel) return true;
-    if (bytes > kLdsMax || hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               static_cast<int>(bytes)) != hipSuccess) {
+    int i = 0;
+    while (i < n && kern[i] != kernel) ++i;
+    if (i < n && size[i] >= bytes) return true;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(bytes)) != hipSuccess) {
         (void)hipGetLastError();
         TECO_ERROR("cannot reserve %zu bytes of LDS for a kernel", bytes);
         return false;
     }
-    if (ndone < 256) done[ndone++] = kernel;
+    if (i < n) {
+        size[i] = bytes;
+    } else if (n < 256) {
+        kern[n] = kernel;
+        size[n++] = bytes;
+    }
     return true;
 }
 
