@@ -26,6 +26,7 @@ struct FaParams {
     int kv_cap;          // block-table width * block_size: kv lengths are clamped to it
     long long page_stride;                      // Hkv * bs * D elements per cache block
     float scale_log2;    // softmax_scale * log2(e)
+    float inv_scale_log2;  // 1 / scale_log2: the rescale test compares raw scores
     int causal;
     long long total_q;   // rows of q and of the output (q's descriptor)
     // split-KV decode

@@ -647,7 +647,9 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
                                             const u32x4 (&qf)[QSUB][D / 16],
                                             f32x16_t (&oacc)[QSUB][D / 32], float (&m)[QSUB],
                                             float (&lsum)[QSUB], const int (&lim)[QSUB],
-                                            float scale_log2, bool mask = MASK) {
+                                            float scale_log2, float inv_scale_log2,
+                                            bool mask = MASK) {
+    const float slack_raw = kRescaleSlack * inv_scale_log2;
     const int lane = threadIdx.x & 63;
     const int g = lane >> 5, r32 = lane & 31;
     f32x16_t s[NKB][QSUB];
@@ -680,11 +682,17 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
                     s[kb][qs][v] = x;
                 }
         }
+        // The rescale test runs on this half-wave's raw scores: every lane's
+        // max of its 16 keys is within the slack exactly when every query
+        // column's max over all 32 keys is, so the exchange with the other
+        // half-wave and the scaling are only needed when the max is raised.
+        // (The test's rounding can differ from that of the scaled max by an
+        // ulp; either outcome is exact, see kRescaleSlack.)
         float mx = max16(s[0][qs]);
 #pragma unroll
         for (int kb = 1; kb < NKB; ++kb) mx = fmaxf(mx, max16(s[kb][qs]));
-        mx = half_swap_max(mx) * scale_log2;
-        if (!__all(mx <= m[qs] + kRescaleSlack)) {
+        if (!__all(mx <= fmaf(m[qs], inv_scale_log2, slack_raw))) {
+            mx = half_swap_max(mx) * scale_log2;
             const float m_new = fmaxf(m[qs], mx);  // m >= 0 keeps the reference clamp
             const float alpha = __builtin_amdgcn_exp2f(m[qs] - m_new);
             m[qs] = m_new;
@@ -829,7 +837,7 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
                 // one copy of the block code; the mask is a uniform branch
                 wave_attend<T, D, KP, VP, NKB, QSUB, true>(cur, cur + TILE * KP, KB * hb, qf, oacc, m,
                                                            lsum, lim, p.scale_log2,
-                                                           j0 + KB > wave_min_vis);
+                                                           p.inv_scale_log2, j0 + KB > wave_min_vis);
             }
         }
         if (it + 1 < ntiles) ld.store(lds + ((it + 1) & 1) * Loader::ELEMS);
@@ -1011,10 +1019,12 @@ __device__ __forceinline__ void decode_pass(const FaParams &p, uint16_t *smem, i
             const int lim[1] = {vis - jw - 4 * g};
             if (jw + 32 > min_vis)
                 wave_attend<T, D, KP, VP, 1, 1, true>(smem, smem + kDecTile * KP, 32 * wave, qf,
-                                                      oacc, m, lsum, lim, p.scale_log2);
+                                                      oacc, m, lsum, lim, p.scale_log2,
+                                                      p.inv_scale_log2);
             else
                 wave_attend<T, D, KP, VP, 1, 1, false>(smem, smem + kDecTile * KP, 32 * wave, qf,
-                                                       oacc, m, lsum, lim, p.scale_log2);
+                                                       oacc, m, lsum, lim, p.scale_log2,
+                                                       p.inv_scale_log2);
         }
     }
 
@@ -1585,6 +1595,7 @@ tecoopsStatus_t fa_prepare(tecoopsHandle_t handle, int max_seqlen_q, int max_seq
     p.page_stride = static_cast<long long>(Hkv) * bs * D;
     const float scale = softmax_scale > 0.0f ? softmax_scale : 1.0f / std::sqrt(static_cast<float>(D));
     p.scale_log2 = scale * 1.4426950408889634f;
+    p.inv_scale_log2 = 1.0f / p.scale_log2;
     p.causal = causal != 0;
 
     // The q bound routes the call (decode or prefill) and sizes the prefill
