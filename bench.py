@@ -71,6 +71,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--ops", default="")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--cases", action="store_true",
+                    help="time the reference's own prototxt cases (harness statistic) instead")
     return ap.parse_args()
 
 
@@ -451,6 +453,132 @@ def _cpu_ops_once(orc, runs):
     return res
 
 
+# ----------------------------------------------------------- reference cases
+
+def _case_tensor(t, gen):
+    """A device tensor for one input of a prototxt case: the case's own values
+    where it gives them (lengths, offsets, indices), else seeded data of its
+    shape, dtype and range (timing does not depend on the values; integer
+    ranges, e.g. slot ids in [-1, 1024), are kept)."""
+    import torch
+    dt = {"DTYPE_HALF": torch.float16, "DTYPE_FLOAT": torch.float32,
+          "DTYPE_INT32": torch.int32, "DTYPE_INT64": torch.int64}[t["dtype"]]
+    shape = t["shape"]["dims"]
+    if "prev_value" in t:
+        vals = t["prev_value"].get("value_i", t["prev_value"].get("value_f"))
+        return torch.tensor(vals, dtype=dt, device="cuda").reshape(shape)
+    r = t.get("random_data", {})
+    lo, hi = float(r.get("lower_bound", -1.0)), float(r.get("upper_bound", 1.0))
+    u = torch.rand(shape, generator=gen, device="cuda") * (hi - lo) + lo
+    return u.floor().to(dt) if not dt.is_floating_point else u.to(dt)
+
+
+def time_cases(repeat=100, warm=10):
+    """The reference's own op test cases (test/zoo/teco/<op>/test_case/
+    *.prototxt, stored as data in tests/golden/prototxt_cases.json), each run
+    through the C entry point the reference harness calls and timed the way
+    the harness reports them (test/src/suite/executor.cpp:228-277): `warm`
+    launches, then `repeat` launches each between its own pair of HIP events,
+    sorted, the fastest and slowest tenth dropped, the rest averaged.  GB/s
+    and TFLOP/s divide the harness's theory_io / theory_ops of each op
+    (executor.cpp:893-913 and the ops' getTheoryIoSize / getTheoryOps:
+    rms_norm.cpp:88-115, reshape_and_cache.cpp:103-114, causal_conv1d.cpp:
+    119-135, flash_attention.cpp:106-114, memset.cpp:62-67).  The harness
+    times kernels with its profiler; events also count each launch's own
+    overhead (~2-5 us), so these small cases read slower than their kernels."""
+    import ctypes
+    import torch
+    import tecoops
+    from tecoops import _lib
+    with open(os.path.join(REPO, "tests", "golden", "prototxt_cases.json")) as f:
+        cases = json.load(f)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2024)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    out = []
+    for op in ("rms_norm", "reshape_and_cache", "flash_attention", "causal_conv1d", "memset"):
+        for c in cases[op]:
+            ins = {t["id"]: _case_tensor(t, gen) for t in c["input"]}
+            prm = next(iter(c.get("tecokernel_param", {}).values()), {})
+            nbytes = lambda t: t.numel() * t.element_size()
+            if op == "rms_norm":
+                x, w, res = ins["input"], ins["weight"], ins.get("residual")
+                N, D = x.shape
+                y, ro = torch.empty_like(x), (torch.empty_like(x) if res is not None else None)
+                eps = float(prm.get("eps", 1e-6))
+                fn = lambda: tecoops.rms_norm(x, w, res, y, ro, eps)
+                io = N * D * 2 + D * 2 + N * D * 2 + (2 * N * D * 2 if res is not None else 0)
+                ops = N * D * 4 + (N * D if res is not None else 0)
+            elif op == "reshape_and_cache":
+                k, v, sl = ins["key"], ins["value"], ins["slot_mapping"]
+                oc = {t["id"]: t["shape"]["dims"] for t in c["output"]}
+                kc = torch.zeros(oc["key_cache"], dtype=torch.float16, device="cuda")
+                vc = torch.zeros_like(kc)
+                fn = lambda: tecoops.reshape_and_cache(k, v, sl, kc, vc)
+                kv = k.numel() * 2
+                io, ops = kv * 2 + sl.numel() * 8 + kv * 2, 0
+            elif op == "flash_attention":
+                bt = (ins["blockTable"] % ins["kCache"].shape[0]).to(torch.int32)
+                q, kc, vc = ins["qData"], ins["kCache"], ins["vCache"]
+                ql, kl = ins["q_seq_lens"].to(torch.int32), ins["kv_seq_lens"].to(torch.int32)
+                o = torch.zeros_like(q)
+                mq, mk = int(prm.get("max_seqlen_q", 0)), int(prm.get("max_seqlen_k", 0))
+                d = lambda t, code: tecoops._Desc(t, code)
+                with d(bt, _lib.DATA_INT32) as btd, d(q, _lib.DATA_HALF) as qd, \
+                        d(kc, _lib.DATA_HALF) as kd, d(vc, _lib.DATA_HALF) as vd, \
+                        d(o, _lib.DATA_HALF) as od:
+                    args = (mq, mk, bt.shape[1], P(ql), P(kl), btd, P(bt), qd, P(q), kd, P(kc), vd,
+                            P(vc), od, P(o), None)
+                    fn = lambda args=args: _lib.call("tecoopsFlashAttention",
+                                                     tecoops._handle(o.device), *args)
+                    out.append(_time_case(c, op, fn, repeat, warm,
+                                          sum(nbytes(t) for t in (bt, q, kc, vc, ql, kl, o)),
+                                          4 * q.shape[0] * int(kl.sum()) * q.shape[2] * q.shape[1]))
+                continue
+            elif op == "causal_conv1d":
+                x, w, st = ins["x"], ins["weight"], ins["convState"]
+                qsl, cidx = ins["query_start_loc"], ins["cache_indices"]
+                hin = ins["has_initial_state"].to(torch.int8)
+                total, dim = x.shape
+                width = w.shape[0]
+                y = torch.empty_like(x)
+                fn = lambda: _lib.call(
+                    "tecoopsCausalConv1d", tecoops._handle(x.device), qsl.numel() - 1, total, dim,
+                    width, int(prm["conv_state_stride"]), int(prm["x_seq_stride"]),
+                    int(prm["out_seq_stride"]), int(prm["pad_slot_id"]), int(prm["api_mode"]),
+                    int(prm["act_mode"]), P(x), P(st), P(w), P(y), P(qsl), P(cidx), P(hin))
+                batch = qsl.numel() - 1
+                io = total * dim * 2 + width * dim * 2 + batch * (width - 1) * dim * 2 * 2 + total * dim * 2
+                ops = total * dim * 20
+            else:  # memset
+                x = ins["x"]
+                size, value = int(prm["size"]), int(prm["value"])
+                fn = lambda: _lib.call("tecoopsMemset", tecoops._handle(x.device), P(x), value, size)
+                io, ops = size, x.numel()
+            out.append(_time_case(c, op, fn, repeat, warm, io, ops))
+    return out
+
+
+def _time_case(c, op, fn, repeat, warm, io, ops):
+    import torch
+    for _ in range(warm):
+        fn()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(2 * repeat)]
+    for i in range(repeat):
+        marks[2 * i].record()
+        fn()
+        marks[2 * i + 1].record()
+    torch.cuda.synchronize()
+    t = sorted(marks[2 * i].elapsed_time(marks[2 * i + 1]) * 1e3 for i in range(repeat))
+    cut = repeat // 10
+    us = sum(t[cut:repeat - cut]) / (repeat - 2 * cut)
+    r = {"case": c["file"].split("test/zoo/teco/")[-1], "op": op, "us": round(us, 3),
+         "theory_io": int(io), "gbs": round(io / us / 1e3, 2)}
+    if ops:
+        r.update(theory_ops=int(ops), tflops=round(ops / us / 1e6, 4))
+    return r
+
+
 def cpu_model():
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
@@ -470,6 +598,11 @@ def main():
         sys.exit(2)
     import torch
     torch.cuda.set_device(0)
+    if args.cases:
+        print(json.dumps({"metric": "reference prototxt cases: trimmed-mean us of 100 launches "
+                                    "(the harness statistic), GB/s and TFLOP/s of its theory_io / "
+                                    "theory_ops", "n_gpus": 1, "cases": time_cases()}), flush=True)
+        return
     keep = set(args.ops.split(",")) if args.ops else None
     ops = build_ops(keep)
     if keep:
