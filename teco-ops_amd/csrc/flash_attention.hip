@@ -21,10 +21,12 @@
 //     of O^T += V^T P^T (the key order inside an MFMA k-step is permuted
 //     consistently on both operands).
 //   * K tiles are staged in LDS row-major with a 16-byte row pad (conflict-free
-//     128-bit A-operand reads); V tiles are staged transposed (V^T[d][key],
-//     4-element pad) so the A operand of the PV product is two 64-bit reads.
-//     Global -> register prefetch of the next tile overlaps the current tile's
-//     MFMA work.
+//     128-bit A-operand reads).  With D = 128 and a paged cache V tiles are
+//     staged row-major too (32-byte pad) and the A operand of the PV product
+//     is two transposing 64-bit reads (ds_read_b64_tr_b16); the other loaders
+//     stage V transposed (V^T[d][key], 4-element pad) so it is two plain
+//     64-bit reads.  Global -> register prefetch of the next tile overlaps
+//     the current tile's MFMA work.
 //   * Prefill (D = 128, block_size a multiple of 8): a workgroup of 12 waves
 //     (3 per SIMD) shares each 96-key K/V tile among up to 4 query heads of
 //     one GQA group (HW heads x (12/HW) row blocks of 32); other shapes use 4
@@ -93,6 +95,12 @@ constexpr float kNegInf = -INFINITY;
 // rescale runs rarely; P <= 2^kRescaleSlack stays exact in fp32 and keeps
 // its relative precision in 16 bit.
 constexpr float kRescaleSlack = 8.0f;
+
+// Pad (elements) of a row-major V row in LDS: each 16-lane group of the PV
+// product's transposing reads takes 4 key rows x 8 dwords, which a row pitch
+// of 72 dwords puts on distinct banks (measured against pads of 8 and 32:
+// prefill 547 vs 554 and 550 us at B4 x 4096).
+constexpr int kVRowPad = 16;
 
 // With q_lens the offset is the sum of the lengths before b, taken by the 64
 // lanes of the wave in parallel (called by every lane of every wave).
@@ -188,6 +196,7 @@ template <int D, int TILE, int NT, int BSM, bool STREAM = false>
 struct TileLoader {
     static constexpr int KP = D + 8;
     static constexpr int VP = TILE + 4;
+    static constexpr int VR = 0;
     static constexpr int ELEMS = TILE * KP + D * VP;  // one K + V^T buffer
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int KTASKS = TILE * CPR;
@@ -287,15 +296,18 @@ struct TileLoader {
 // (lane l: rows 2*(l%4) + {0,1}, column block l/4), so the cache block
 // holding an instruction's rows is the same for the whole wave: its id is a
 // scalar, read from the block table one load() call ahead (prefetch), so the
-// global loads never wait for it.  Same LDS layout as TileLoader: K [TILE][D +
-// 8], V^T [D][TILE + 4].  load() must be called for consecutive tiles after
-// one prefetch() of the first.
+// global loads never wait for it.  K and V are both stored row-major, [TILE]
+// [D + 8] and [TILE][D + kVRowPad] (VP = 0, VR = row pitch tells wave_attend
+// so): V is not transposed on the way in, the PV product reads it with
+// transposing LDS reads.  load() must be
+// called for consecutive tiles after one prefetch() of the first.
 template <int TILE, int W, int BSM, bool STREAM = false>
 struct PagedLoader128 {
     static constexpr int D = 128;
     static constexpr int KP = D + 8;
-    static constexpr int VP = TILE + 4;
-    static constexpr int ELEMS = TILE * KP + D * VP;
+    static constexpr int VP = 0;
+    static constexpr int VR = D + kVRowPad;
+    static constexpr int ELEMS = TILE * (KP + VR);
     static constexpr int RW = TILE / W;     // rows per wave
     static constexpr int KI = RW / 4;       // K load instructions per wave
     static constexpr int VI = RW / 8;       // V load instruction pairs per wave
@@ -367,7 +379,7 @@ struct PagedLoader128 {
 
     __device__ __forceinline__ void store(uint16_t *buf) const {
         uint16_t *Ks = buf;
-        uint16_t *Vt = buf + TILE * KP;
+        uint16_t *Vs = buf + TILE * KP;
         const int lane = threadIdx.x & 63;
         const int w = threadIdx.x >> 6;
         const int kr = lane >> 4, kc = lane & 15;
@@ -379,16 +391,9 @@ struct PagedLoader128 {
         for (int i = 0; i < VI; ++i) {
             const int r = w * RW + 8 * i + vr;
             const u32x4 zero = {0u, 0u, 0u, 0u};
-            const u32x4 a = (vok >> (2 * i)) & 1u ? v[i][0] : zero;
-            const u32x4 b = (vok >> (2 * i + 1)) & 1u ? v[i][1] : zero;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // columns d = 8vc + 2e (low halves) and 8vc + 2e + 1 (high halves)
-                const uint32_t lo = __builtin_amdgcn_perm(b[e], a[e], 0x05040100u);
-                const uint32_t hi = __builtin_amdgcn_perm(b[e], a[e], 0x07060302u);
-                *reinterpret_cast<uint32_t *>(Vt + (8 * vc + 2 * e) * VP + r) = lo;
-                *reinterpret_cast<uint32_t *>(Vt + (8 * vc + 2 * e + 1) * VP + r) = hi;
-            }
+            *reinterpret_cast<u32x4 *>(Vs + r * VR + vc * 8) = (vok >> (2 * i)) & 1u ? v[i][0] : zero;
+            *reinterpret_cast<u32x4 *>(Vs + (r + 1) * VR + vc * 8) =
+                (vok >> (2 * i + 1)) & 1u ? v[i][1] : zero;
         }
     }
 };
@@ -403,6 +408,7 @@ struct PagedLoader64 {
     static constexpr int D = 64;
     static constexpr int KP = D + 8;
     static constexpr int VP = TILE + 4;
+    static constexpr int VR = 0;
     static constexpr int ELEMS = TILE * KP + D * VP;
     static constexpr int RW = TILE / W;     // rows per wave
     static constexpr int KI = RW / 8;       // K load instructions per wave
@@ -497,6 +503,7 @@ struct PagedLoader96 {
     static constexpr int D = 96;
     static constexpr int KP = D + 8;
     static constexpr int VP = TILE + 4;
+    static constexpr int VR = 0;
     static constexpr int ELEMS = TILE * KP + D * VP;
     static constexpr int RW = TILE / W;     // rows per wave
     static constexpr int KI = RW / 4;       // K load instructions per wave
@@ -625,6 +632,15 @@ template <> struct Ones2<f16> {
     }
 };
 
+// ds_read_b64_tr_b16: 8 bytes per lane, transposed within each 16-lane group
+// (see the row-major V read in wave_attend).
+__device__ __forceinline__ u32x2 tr_b16_b64(const uint16_t *p) {
+    typedef short i16x4_t __attribute__((ext_vector_type(4)));
+    const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4_t *)(p));
+    return __builtin_bit_cast(u32x2, v);
+}
+
 // Max of one lane's 16 scores as a tree of three-input maxima (v_max3_f32):
 // 8 instructions, 3 deep.
 __device__ __forceinline__ float max16(const f32x16_t &s) {
@@ -642,7 +658,7 @@ __device__ __forceinline__ float max16(const f32x16_t &s) {
 //   m:    running max (log2 domain, >= 0), lsum: this half-wave's partial sum of P
 //   lim:  key r (0-based in the staged rows, r = 32kb + 8(v/4) + 4(l/32) + v%4)
 //         is visible when r - 4(l/32) < lim[qs]
-template <typename T, int D, int KP, int VP, int NKB, int QSUB, bool MASK>
+template <typename T, int D, int KP, int VP, int VR, int NKB, int QSUB, bool MASK>
 __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *Vt, int kv_row0,
                                             const u32x4 (&qf)[QSUB][D / 16],
                                             f32x16_t (&oacc)[QSUB][D / 32], float (&m)[QSUB],
@@ -650,6 +666,11 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
                                             float scale_log2, float inv_scale_log2,
                                             bool mask = MASK) {
     const float slack_raw = kRescaleSlack * inv_scale_log2;
+    // row-major V (pitch VR): this lane's element offset for the transposing
+    // reads, key 4g + s / 4 and head dim 16 (G % 2) + 4 (s % 4) of a 16-key,
+    // 32-dim block (G = lane / 16, s = lane % 16)
+    const int vlane = (4 * (threadIdx.x >> 5 & 1) + ((threadIdx.x & 15) >> 2)) * VR +
+                      16 * (threadIdx.x >> 4 & 1) + 4 * (threadIdx.x & 3);
     const int lane = threadIdx.x & 63;
     const int g = lane >> 5, r32 = lane & 31;
     f32x16_t s[NKB][QSUB];
@@ -728,10 +749,24 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
         }
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) {
-            const uint16_t *vr = Vt + (32 * db + r32) * VP + kv_row0 + 16 * t + 4 * g;
-            const u32x2 lo2 = *reinterpret_cast<const u32x2 *>(vr);
-            const u32x2 hi2 = *reinterpret_cast<const u32x2 *>(vr + 8);
-            const u32x4 a = {lo2.x, lo2.y, hi2.x, hi2.y};
+            u32x4 a;
+            if constexpr (VR > 0) {
+                // V row-major [key][VR]: each 16-lane group of a
+                // ds_read_b64_tr_b16 hands lane i value i % 4 of the group's
+                // lanes i / 4 + {0, 4, 8, 12}; lane s points at key s / 4 and
+                // head dims 4 (s % 4) .. +3 of its group's 16, so lane i gets
+                // head dim d0 + i of 4 consecutive keys (the A operand's k
+                // order of the V^T layout below)
+                const uint16_t *vb = Vt + (kv_row0 + 16 * t) * VR + 32 * db + vlane;
+                const u32x2 lo2 = tr_b16_b64(vb);
+                const u32x2 hi2 = tr_b16_b64(vb + 8 * VR);
+                a = u32x4{lo2.x, lo2.y, hi2.x, hi2.y};
+            } else {
+                const uint16_t *vr = Vt + (32 * db + r32) * VP + kv_row0 + 16 * t + 4 * g;
+                const u32x2 lo2 = *reinterpret_cast<const u32x2 *>(vr);
+                const u32x2 hi2 = *reinterpret_cast<const u32x2 *>(vr + 8);
+                a = u32x4{lo2.x, lo2.y, hi2.x, hi2.y};
+            }
 #pragma unroll
             for (int qs = 0; qs < QSUB; ++qs) oacc[qs][db] = Mma<T>::run(a, pf[qs], oacc[qs][db]);
         }
@@ -748,6 +783,16 @@ __device__ __forceinline__ void store_row4(uint16_t *dst, float a, float b, floa
 
 // ---------------------------------------------------------------- prefill
 
+// Elements of one staged K/V tile of TILE keys: K [TILE][D + 8] and V either
+// transposed [D][TILE + 4] or row-major [TILE][D + kVRowPad], whichever the
+// loader uses (the larger of the two).
+template <int D, int TILE>
+constexpr size_t kv_tile_elems() {
+    constexpr size_t vt = static_cast<size_t>(D) * (TILE + 4),
+                     vr = static_cast<size_t>(TILE) * (D + kVRowPad);
+    return static_cast<size_t>(TILE) * (D + 8) + (vt > vr ? vt : vr);
+}
+
 // Padded LDS row of the staged O rows of a prefill workgroup (HW heads x D
 // values): the pad spreads the 8-byte fragment writes of consecutive rows
 // over the banks.
@@ -760,7 +805,7 @@ constexpr int o_row() {
 // staged O rows ([32*QSUB*(W/HW)][o_row]) reuse at the end of the tile.
 template <int D, int TILE, int W, int HW, int QSUB>
 constexpr size_t prefill_lds_bytes() {
-    constexpr size_t kv = 2 * (TILE * (D + 8) + D * (TILE + 4));
+    constexpr size_t kv = 2 * kv_tile_elems<D, TILE>();
     constexpr size_t o = static_cast<size_t>(32 * QSUB * (W / HW)) * o_row<D, HW>();
     return sizeof(uint16_t) * (kv > o ? kv : o);
 }
@@ -774,7 +819,7 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
     constexpr int NKB = TILE % 64 == 0 ? 2 : 1;
     constexpr int KB = 32 * NKB;
     using Loader = typename LoaderSel<D, TILE, W, BSM>::type;
-    constexpr int KP = Loader::KP, VP = Loader::VP;
+    constexpr int KP = Loader::KP, VP = Loader::VP, VR = Loader::VR;
     constexpr int WROWS = 32 * QSUB;
     constexpr int QT = WROWS * (W / HW);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -835,7 +880,7 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
 #pragma unroll
                 for (int qs = 0; qs < QSUB; ++qs) lim[qs] = vis[qs] - j0 - 4 * g;
                 // one copy of the block code; the mask is a uniform branch
-                wave_attend<T, D, KP, VP, NKB, QSUB, true>(cur, cur + TILE * KP, KB * hb, qf, oacc, m,
+                wave_attend<T, D, KP, VP, VR, NKB, QSUB, true>(cur, cur + TILE * KP, KB * hb, qf, oacc, m,
                                                            lsum, lim, p.scale_log2,
                                                            p.inv_scale_log2, j0 + KB > wave_min_vis);
             }
@@ -957,7 +1002,7 @@ constexpr int kDecTile = 128;
 
 template <int D>
 constexpr size_t decode_lds_bytes() {
-    return sizeof(uint16_t) * (kDecTile * (D + 8) + D * (kDecTile + 4));
+    return sizeof(uint16_t) * kv_tile_elems<D, kDecTile>();
 }
 
 // The 4 waves of a decode workgroup attend keys [kv_lo, kv_hi) of (sequence
@@ -971,7 +1016,7 @@ __device__ __forceinline__ void decode_pass(const FaParams &p, uint16_t *smem, i
                                             long long q_off, int L, int S, int kv_lo, int kv_hi,
                                             int rq, int r0) {
     using Loader = typename LoaderSel<D, kDecTile, 4, BSM, true>::type;
-    constexpr int KP = Loader::KP, VP = Loader::VP;
+    constexpr int KP = Loader::KP, VP = Loader::VP, VR = Loader::VR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 5, r32 = lane & 31;
     const int hl = r32 / rq, row = r0 + r32 % rq;
@@ -1018,11 +1063,11 @@ __device__ __forceinline__ void decode_pass(const FaParams &p, uint16_t *smem, i
         if (jw < kv_hi) {
             const int lim[1] = {vis - jw - 4 * g};
             if (jw + 32 > min_vis)
-                wave_attend<T, D, KP, VP, 1, 1, true>(smem, smem + kDecTile * KP, 32 * wave, qf,
+                wave_attend<T, D, KP, VP, VR, 1, 1, true>(smem, smem + kDecTile * KP, 32 * wave, qf,
                                                       oacc, m, lsum, lim, p.scale_log2,
                                                       p.inv_scale_log2);
             else
-                wave_attend<T, D, KP, VP, 1, 1, false>(smem, smem + kDecTile * KP, 32 * wave, qf,
+                wave_attend<T, D, KP, VP, VR, 1, 1, false>(smem, smem + kDecTile * KP, 32 * wave, qf,
                                                        oacc, m, lsum, lim, p.scale_log2,
                                                        p.inv_scale_log2);
         }
