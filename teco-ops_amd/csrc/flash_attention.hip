@@ -20,12 +20,16 @@
 //     other half-wave.  P^T stays in registers and is directly the B operand
 //     of O^T += V^T P^T (the key order inside an MFMA k-step is permuted
 //     consistently on both operands).
-//   * K tiles are staged in LDS row-major with a 16-byte row pad (conflict-free
-//     128-bit A-operand reads).  With D = 128 and a paged cache V tiles are
-//     staged row-major too (32-byte pad) and the A operand of the PV product
-//     is two transposing 64-bit reads (ds_read_b64_tr_b16); the other loaders
-//     stage V transposed (V^T[d][key], 4-element pad) so it is two plain
-//     64-bit reads.  Global -> register prefetch of the next tile overlaps
+//   * Prefill with D = 128 and a paged cache (block_size a multiple of 8):
+//     K and V tiles go from HBM straight into LDS (global_load_lds_dwordx4,
+//     no registers), two tiles ahead in a ring of three buffers, in a layout
+//     of 4-row blocks (rows chunk-major, 64-byte pad per block) on which the
+//     128-bit K reads and the transposing V reads (ds_read_b64_tr_b16, the A
+//     operand of the PV product) are conflict-free.  Decode with D = 128
+//     stages K and V row-major through registers (16- and 32-byte row pads),
+//     with the same transposing V reads.  The other loaders stage K row-major
+//     (16-byte pad) and V transposed (V^T[d][key], 4-element pad, two plain
+//     64-bit reads).  Global -> register prefetch of the next tile overlaps
 //     the current tile's MFMA work.
 //   * Prefill (D = 128, block_size a multiple of 8): a workgroup of 12 waves
 //     (3 per SIMD) shares each 96-key K/V tile among up to 4 query heads of
@@ -197,6 +201,9 @@ struct TileLoader {
     static constexpr int KP = D + 8;
     static constexpr int VP = TILE + 4;
     static constexpr int VR = 0;
+    static constexpr int VOFF = TILE * KP;  // V region of a tile buffer
+    static constexpr bool DMA = false;
+    static constexpr int STAGES = 2;  // tile buffers in LDS
     static constexpr int ELEMS = TILE * KP + D * VP;  // one K + V^T buffer
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int KTASKS = TILE * CPR;
@@ -307,6 +314,9 @@ struct PagedLoader128 {
     static constexpr int KP = D + 8;
     static constexpr int VP = 0;
     static constexpr int VR = D + kVRowPad;
+    static constexpr int VOFF = TILE * KP;
+    static constexpr bool DMA = false;
+    static constexpr int STAGES = 2;  // tile buffers in LDS
     static constexpr int ELEMS = TILE * (KP + VR);
     static constexpr int RW = TILE / W;     // rows per wave
     static constexpr int KI = RW / 4;       // K load instructions per wave
@@ -398,6 +408,92 @@ struct PagedLoader128 {
     }
 };
 
+// Bytes of one 4-row block of the prefill's D = 128 DMA tile layout: 4 key
+// rows of 256 bytes stored chunk-major (16-byte chunk c of row j at 64c +
+// 16j), then a 64-byte pad.  One global_load_lds_dwordx4 fills a block (lane
+// l's 16 bytes land at 16l), the 128-bit K reads of 16 consecutive rows and
+// the transposing V reads of each half-wave fall on distinct banks, and the
+// fragment offsets stay additive (instruction offsets).
+constexpr int kLdsBlockBytes = 1088;
+
+// 16 zero bytes: the source of V rows past the end of a sequence.
+__device__ __attribute__((aligned(16))) const uint32_t kZero16[4] = {0u, 0u, 0u, 0u};
+
+// HBM -> LDS with no register staging: 16 bytes per lane into
+// dst + 16 * lane (dst wave-uniform, in M0).  Inline assembly on purpose:
+// through the builtin the compiler treats every transposing LDS read as
+// possibly reading the copy's destination and waits for all copies in flight
+// before each one, which serialises the next tile's copy with this tile's
+// work.  Here the copies are ordered by wait_dma() and the workgroup barrier
+// after it.  No other code of these kernels uses M0.
+__device__ __forceinline__ void dma16(const void *src, void *dst) {
+    const uint32_t lds = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)(dst)));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+                 : "memory");
+}
+
+// Prefill loader for D = 128 and a block_size that is a multiple of 8: K and
+// V go from the paged caches straight into LDS (global_load_lds_dwordx4), in
+// the 4-row block layout above, so the tile costs no registers and no LDS
+// stores.  Wave w stages rows [w*RW, (w+1)*RW) of the tile, 4 aligned rows
+// per instruction (lane l: row l % 4, chunk l / 4), whose cache block is the
+// same for the whole wave: its id is a scalar, read from the block table one
+// load() ahead.  V rows at or past kv_limit are read from kZero16; K rows
+// there are read from some cache row and masked in the softmax.  load()
+// issues the copies into a tile buffer, wait_tiles() waits for them (the
+// caller's barrier then publishes the tile).
+template <int TILE, int W, int BSM>
+struct PagedLoaderDma128 {
+    static constexpr int D = 128;
+    static constexpr bool DMA = true;
+    static constexpr int KP = 0, VP = 0, VR = 0;      // the block layout
+    static constexpr int VOFF = TILE / 4 * kLdsBlockBytes / 2;  // elements
+    static constexpr int ELEMS = 2 * VOFF;
+    static constexpr int RW = TILE / W;  // rows per wave
+    static constexpr int KI = RW / 4;    // 4-row blocks per wave
+    static constexpr int STAGES = 3;     // tile buffers: copies run two tiles ahead
+    static constexpr int PER_TILE = 2 * KI;  // copy instructions per tile and lane
+    static_assert(RW % 4 == 0, "each wave stages whole 4-row blocks");
+    static_assert(PER_TILE < 16, "vmcnt immediate");
+    int pg[KI];  // cache block ids of the next load()'s row groups (uniform)
+
+    __device__ __forceinline__ void prefetch(const FaParams &p, const int *bt_row, int j0,
+                                             int kv_limit) {
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < KI; ++i)
+            pg[i] = PagedLoader128<TILE, W, BSM>::group_page(p, bt_row, j0 + w * RW + 4 * i, kv_limit);
+    }
+
+    __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
+                                         int j0, int kv_limit, uint16_t *dst) {
+        const int lane = threadIdx.x & 63;
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int r = lane & 3, c = lane >> 2;
+        char *kd = reinterpret_cast<char *>(dst) + w * KI * kLdsBlockBytes;
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int row0 = j0 + w * RW + 4 * i;
+            const long long off =
+                PagedLoader128<TILE, W, BSM>::group_base(p, head_off, row0, pg[i]) + r * D + c * 8;
+            dma16(p.kc + off, kd + i * kLdsBlockBytes);
+            dma16(row0 + r < kv_limit ? static_cast<const void *>(p.vc + off)
+                                      : static_cast<const void *>(kZero16),
+                  kd + 2 * VOFF + i * kLdsBlockBytes);
+        }
+        prefetch(p, bt_row, j0 + TILE, kv_limit);
+    }
+
+    // Waits until this wave has at most NEWER tiles' copies in flight, i.e.
+    // the tile issued before them has landed (vector memory counter; no
+    // other vector loads are in flight in the tile loop).
+    template <int NEWER>
+    static __device__ __forceinline__ void wait_tiles() {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (NEWER * PER_TILE));
+    }
+};
+
 // The same scheme for D = 64: each K load instruction covers 8 aligned rows
 // (8 lanes x 16 bytes per row); each V instruction covers two 8-row groups,
 // one per half-wave (lane l: rows 8*(l/32) + 2*(l%4) + {0,1}, column block
@@ -409,6 +505,9 @@ struct PagedLoader64 {
     static constexpr int KP = D + 8;
     static constexpr int VP = TILE + 4;
     static constexpr int VR = 0;
+    static constexpr int VOFF = TILE * KP;  // V region of a tile buffer
+    static constexpr bool DMA = false;
+    static constexpr int STAGES = 2;  // tile buffers in LDS
     static constexpr int ELEMS = TILE * KP + D * VP;
     static constexpr int RW = TILE / W;     // rows per wave
     static constexpr int KI = RW / 8;       // K load instructions per wave
@@ -504,6 +603,9 @@ struct PagedLoader96 {
     static constexpr int KP = D + 8;
     static constexpr int VP = TILE + 4;
     static constexpr int VR = 0;
+    static constexpr int VOFF = TILE * KP;  // V region of a tile buffer
+    static constexpr bool DMA = false;
+    static constexpr int STAGES = 2;  // tile buffers in LDS
     static constexpr int ELEMS = TILE * KP + D * VP;
     static constexpr int RW = TILE / W;     // rows per wave
     static constexpr int KI = RW / 4;       // K load instructions per wave
@@ -601,6 +703,15 @@ template <int TILE, int W, bool STREAM>
 struct LoaderSel<128, TILE, W, 2, STREAM> {
     using type = PagedLoader128<TILE, W, 2, STREAM>;
 };
+// prefill (K/V re-read from L2 by every query tile): LDS DMA, no registers
+template <int TILE, int W>
+struct LoaderSel<128, TILE, W, 1, false> {
+    using type = PagedLoaderDma128<TILE, W, 1>;
+};
+template <int TILE, int W>
+struct LoaderSel<128, TILE, W, 2, false> {
+    using type = PagedLoaderDma128<TILE, W, 2>;
+};
 template <int TILE, int W, bool STREAM>
 struct LoaderSel<64, TILE, W, 1, STREAM> {
     using type = PagedLoader64<TILE, W, 1, STREAM>;
@@ -673,6 +784,14 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
                       16 * (threadIdx.x >> 4 & 1) + 4 * (threadIdx.x & 3);
     const int lane = threadIdx.x & 63;
     const int g = lane >> 5, r32 = lane & 31;
+    // the 4-row block layout (KP == 0), byte offsets of this lane: K row r32,
+    // chunk g; V (transposing reads as above) key 4g + s / 4, head dims 16 (G
+    // % 2) + 4 (s % 4) .. +3
+    const int kblane = (r32 >> 2) * kLdsBlockBytes + 16 * (r32 & 3) + 64 * g;
+    const int vblane = g * kLdsBlockBytes + 16 * ((lane & 15) >> 2) + 128 * (lane >> 4 & 1) +
+                       64 * (lane >> 1 & 1) + 8 * (lane & 1);
+    const char *Kb = reinterpret_cast<const char *>(Ks) + (kv_row0 >> 2) * kLdsBlockBytes;
+    const char *Vb = reinterpret_cast<const char *>(Vt) + (kv_row0 >> 2) * kLdsBlockBytes;
     f32x16_t s[NKB][QSUB];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
@@ -684,8 +803,11 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-            const u32x4 a = *reinterpret_cast<const u32x4 *>(
-                Ks + (kv_row0 + 32 * kb + r32) * KP + 16 * ks + 8 * g);
+            const u32x4 a =
+                KP == 0 ? *reinterpret_cast<const u32x4 *>(Kb + kblane + 8 * kb * kLdsBlockBytes +
+                                                           128 * ks)
+                        : *reinterpret_cast<const u32x4 *>(
+                              Ks + (kv_row0 + 32 * kb + r32) * KP + 16 * ks + 8 * g);
 #pragma unroll
             for (int qs = 0; qs < QSUB; ++qs) s[kb][qs] = Mma<T>::run(a, qf[qs][ks], s[kb][qs]);
         }
@@ -750,7 +872,13 @@ __device__ __forceinline__ void wave_attend(const uint16_t *Ks, const uint16_t *
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) {
             u32x4 a;
-            if constexpr (VR > 0) {
+            if constexpr (KP == 0) {
+                const char *vb = Vb + vblane + 4 * t * kLdsBlockBytes + 256 * db;
+                const u32x2 lo2 = tr_b16_b64(reinterpret_cast<const uint16_t *>(vb));
+                const u32x2 hi2 =
+                    tr_b16_b64(reinterpret_cast<const uint16_t *>(vb + 2 * kLdsBlockBytes));
+                a = u32x4{lo2.x, lo2.y, hi2.x, hi2.y};
+            } else if constexpr (VR > 0) {
                 // V row-major [key][VR]: each 16-lane group of a
                 // ds_read_b64_tr_b16 hands lane i value i % 4 of the group's
                 // lanes i / 4 + {0, 4, 8, 12}; lane s points at key s / 4 and
@@ -801,11 +929,12 @@ constexpr int o_row() {
     return HW * D + 8;
 }
 
-// LDS of a prefill workgroup: the double-buffered K/V tiles, which the
+// LDS of a prefill workgroup: the loader's K/V tile buffers, which the
 // staged O rows ([32*QSUB*(W/HW)][o_row]) reuse at the end of the tile.
-template <int D, int TILE, int W, int HW, int QSUB>
+template <int D, int TILE, int W, int HW, int QSUB, int BSM>
 constexpr size_t prefill_lds_bytes() {
-    constexpr size_t kv = 2 * kv_tile_elems<D, TILE>();
+    using Loader = typename LoaderSel<D, TILE, W, BSM>::type;
+    constexpr size_t kv = static_cast<size_t>(Loader::STAGES) * Loader::ELEMS;
     constexpr size_t o = static_cast<size_t>(32 * QSUB * (W / HW)) * o_row<D, HW>();
     return sizeof(uint16_t) * (kv > o ? kv : o);
 }
@@ -863,15 +992,41 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
 
     Loader ld;
     const int ntiles = (kv_end + TILE - 1) / TILE;
+    // Tile t lives in LDS buffer t % NS.  A DMA loader copies straight into
+    // the buffer (NS = 3: tile t + 2 is copied while tile t is attended), the
+    // others stage tile t + 1 in registers and store it after tile t (NS = 2).
+    constexpr int NS = Loader::STAGES;
+    // (the offset goes through readfirstlane so that it stays one scalar:
+    // otherwise the compiler precomputes lane addresses for every buffer)
+    auto buf = [&](int t) { return lds + __builtin_amdgcn_readfirstlane((t % NS) * Loader::ELEMS); };
+    auto load = [&](int t) {
+        if constexpr (Loader::DMA)
+            ld.load(p, bt_row, head_off, t * TILE, S, buf(t));
+        else
+            ld.load(p, bt_row, head_off, t * TILE, S);
+    };
+    // tile t is in LDS for this wave (the barrier after it publishes it)
+    auto land = [&](int t) {
+        if constexpr (Loader::DMA) {
+            if (NS > 2 && t + 1 < ntiles)
+                Loader::template wait_tiles<1>();
+            else
+                Loader::template wait_tiles<0>();
+        } else {
+            ld.store(buf(t));
+        }
+    };
     if (ntiles > 0) {
         ld.prefetch(p, bt_row, 0, S);
-        ld.load(p, bt_row, head_off, 0, S);
-        ld.store(lds);
+        load(0);
+        if constexpr (NS > 2)
+            if (ntiles > 1) load(1);
+        land(0);
     }
     __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
-        const uint16_t *cur = lds + (it & 1) * Loader::ELEMS;
-        if (it + 1 < ntiles) ld.load(p, bt_row, head_off, (it + 1) * TILE, S);
+        const uint16_t *cur = buf(it);
+        if (it + NS - 1 < ntiles) load(it + NS - 1);
 #pragma unroll
         for (int hb = 0; hb < TILE / KB; ++hb) {
             const int j0 = it * TILE + KB * hb;
@@ -880,12 +1035,12 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
 #pragma unroll
                 for (int qs = 0; qs < QSUB; ++qs) lim[qs] = vis[qs] - j0 - 4 * g;
                 // one copy of the block code; the mask is a uniform branch
-                wave_attend<T, D, KP, VP, VR, NKB, QSUB, true>(cur, cur + TILE * KP, KB * hb, qf, oacc, m,
+                wave_attend<T, D, KP, VP, VR, NKB, QSUB, true>(cur, cur + Loader::VOFF, KB * hb, qf, oacc, m,
                                                            lsum, lim, p.scale_log2,
                                                            p.inv_scale_log2, j0 + KB > wave_min_vis);
             }
         }
-        if (it + 1 < ntiles) ld.store(lds + ((it + 1) & 1) * Loader::ELEMS);
+        if (it + 1 < ntiles) land(it + 1);
         __syncthreads();
     }
 
@@ -897,8 +1052,8 @@ __device__ __forceinline__ void prefill_tile(const FaParams &p, uint16_t *lds, i
     constexpr int OROW = o_row<D, HW>();
     constexpr int RCH = HW * D / 8;  // 16-byte chunks per row
     constexpr int NOC = (QT * RCH + W * 64 - 1) / (W * 64);
-    static_assert(2 * Loader::ELEMS * sizeof(uint16_t) <= prefill_lds_bytes<D, TILE, W, HW, QSUB>() &&
-                      QT * OROW * sizeof(uint16_t) <= prefill_lds_bytes<D, TILE, W, HW, QSUB>(),
+    static_assert(NS * Loader::ELEMS * sizeof(uint16_t) <= prefill_lds_bytes<D, TILE, W, HW, QSUB, BSM>() &&
+                      QT * OROW * sizeof(uint16_t) <= prefill_lds_bytes<D, TILE, W, HW, QSUB, BSM>(),
                   "K/V tiles and staged O rows fit the workgroup's LDS");
 #pragma unroll
     for (int qs = 0; qs < QSUB; ++qs) {
@@ -1063,11 +1218,11 @@ __device__ __forceinline__ void decode_pass(const FaParams &p, uint16_t *smem, i
         if (jw < kv_hi) {
             const int lim[1] = {vis - jw - 4 * g};
             if (jw + 32 > min_vis)
-                wave_attend<T, D, KP, VP, VR, 1, 1, true>(smem, smem + kDecTile * KP, 32 * wave, qf,
+                wave_attend<T, D, KP, VP, VR, 1, 1, true>(smem, smem + Loader::VOFF, 32 * wave, qf,
                                                       oacc, m, lsum, lim, p.scale_log2,
                                                       p.inv_scale_log2);
             else
-                wave_attend<T, D, KP, VP, VR, 1, 1, false>(smem, smem + kDecTile * KP, 32 * wave, qf,
+                wave_attend<T, D, KP, VP, VR, 1, 1, false>(smem, smem + Loader::VOFF, 32 * wave, qf,
                                                        oacc, m, lsum, lim, p.scale_log2,
                                                        p.inv_scale_log2);
         }
@@ -1422,7 +1577,7 @@ template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
 tecoopsStatus_t launch_prefill(const FaParams &p, const Plan &pl, hipStream_t s) {
     constexpr int QT = 32 * QSUB * (W / HW);
     auto *kern = &fa_prefill_kernel<T, D, W, HW, QSUB, BSM, TILE>;
-    const size_t lds = prefill_lds_bytes<D, TILE, W, HW, QSUB>();
+    const size_t lds = prefill_lds_bytes<D, TILE, W, HW, QSUB, BSM>();
     if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), lds))
         return TECOOPS_STATUS_INTERNAL_ERROR;
     const int units = p.batch * p.Hkv * (p.G / HW);
