@@ -297,6 +297,31 @@ struct TileLoader {
     }
 };
 
+// Block id of the aligned row group (a multiple of 4 rows inside one cache
+// block) starting at `row0` (wave-uniform), or 0 past kv_limit.  The block
+// table is read-only for the launch: read through the constant address space,
+// the wave-uniform entry is always a scalar load, so waiting for it never
+// waits for the K/V vector loads in flight (a vector load here would, under
+// s_waitcnt vmcnt).
+template <int BSM>
+__device__ __forceinline__ int uniform_group_page(const FaParams &p, const int *bt_row, int row0,
+                                                  int kv_limit) {
+    row0 = __builtin_amdgcn_readfirstlane(row0);
+    const auto *bt4 = (const __attribute__((address_space(4))) int *)(bt_row);
+    return row0 < kv_limit ? bt4[block_of<BSM>(p, row0)] : 0;
+}
+
+// Element offset of such a group's first row (page 0 when its id is out of
+// range).
+template <int D, int BSM>
+__device__ __forceinline__ long long uniform_group_base(const FaParams &p, long long head_off,
+                                                        int row0, int page) {
+    if (page < 0 || page >= p.num_blocks) page = 0;
+    return static_cast<long long>(page) * p.page_stride + head_off +
+           static_cast<long long>(BSM == 1 ? row0 & (p.bs - 1)
+                                            : row0 - block_of<BSM>(p, row0) * p.bs) * D;
+}
+
 // Loader for D = 128 and a block_size that is a multiple of 8.  Wave w stages rows
 // [w*RW, (w+1)*RW) of the tile.  Each K load instruction covers 4 aligned rows
 // (16 lanes x 16 bytes per row) and each V load instruction 8 aligned rows
@@ -327,26 +352,13 @@ struct PagedLoader128 {
     uint32_t vok;     // bit 2i+j: V row of v[i][j] is below kv_limit
     int pg[KI + VI];  // cache block ids of the next load()'s row groups (uniform)
 
-    // Block id of the aligned row group starting at `row0` (wave-uniform), or
-    // 0 past kv_limit.
     static __device__ __forceinline__ int group_page(const FaParams &p, const int *bt_row,
                                                      int row0, int kv_limit) {
-        row0 = __builtin_amdgcn_readfirstlane(row0);
-        // The block table is read-only for the launch: read through the
-        // constant address space, the wave-uniform entry is always a scalar
-        // load, so waiting for it never waits for the K/V vector loads in
-        // flight (a vector load here would, under s_waitcnt vmcnt).
-        const auto *bt4 = (const __attribute__((address_space(4))) int *)(bt_row);
-        return row0 < kv_limit ? bt4[block_of<BSM>(p, row0)] : 0;
+        return uniform_group_page<BSM>(p, bt_row, row0, kv_limit);
     }
-
-    // Element offset of the group's first row (page 0 when its id is out of range).
     static __device__ __forceinline__ long long group_base(const FaParams &p, long long head_off,
                                                            int row0, int page) {
-        if (page < 0 || page >= p.num_blocks) page = 0;
-        return static_cast<long long>(page) * p.page_stride + head_off +
-               static_cast<long long>(BSM == 1 ? row0 & (p.bs - 1)
-                                                : row0 - block_of<BSM>(p, row0) * p.bs) * D;
+        return uniform_group_base<D, BSM>(p, head_off, row0, page);
     }
 
     __device__ __forceinline__ void prefetch(const FaParams &p, const int *bt_row, int j0,
@@ -463,7 +475,7 @@ struct PagedLoaderDma128 {
         const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
         for (int i = 0; i < KI; ++i)
-            pg[i] = PagedLoader128<TILE, W, BSM>::group_page(p, bt_row, j0 + w * RW + 4 * i, kv_limit);
+            pg[i] = uniform_group_page<BSM>(p, bt_row, j0 + w * RW + 4 * i, kv_limit);
     }
 
     __device__ __forceinline__ void load(const FaParams &p, const int *bt_row, long long head_off,
@@ -476,7 +488,7 @@ struct PagedLoaderDma128 {
         for (int i = 0; i < KI; ++i) {
             const int row0 = j0 + w * RW + 4 * i;
             const long long off =
-                PagedLoader128<TILE, W, BSM>::group_base(p, head_off, row0, pg[i]) + r * D + c * 8;
+                uniform_group_base<D, BSM>(p, head_off, row0, pg[i]) + r * D + c * 8;
             dma16(p.kc + off, kd + i * kLdsBlockBytes);
             dma16(row0 + r < kv_limit ? static_cast<const void *>(p.vc + off)
                                       : static_cast<const void *>(kZero16),
@@ -523,12 +535,10 @@ struct PagedLoader64 {
         const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
         for (int i = 0; i < KI; ++i)
-            pg[i] = PagedLoader128<TILE, W, BSM, STREAM>::group_page(p, bt_row, j0 + w * RW + 8 * i,
-                                                                kv_limit);
+            pg[i] = uniform_group_page<BSM>(p, bt_row, j0 + w * RW + 8 * i, kv_limit);
 #pragma unroll
         for (int i = 0; i < 2 * VI; ++i)
-            pg[KI + i] = PagedLoader128<TILE, W, BSM, STREAM>::group_page(p, bt_row,
-                                                                     j0 + w * RW + 8 * i, kv_limit);
+            pg[KI + i] = uniform_group_page<BSM>(p, bt_row, j0 + w * RW + 8 * i, kv_limit);
     }
 
     static __device__ __forceinline__ long long group_base(const FaParams &p, long long head_off,
@@ -621,12 +631,10 @@ struct PagedLoader96 {
         const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
         for (int i = 0; i < KI; ++i)
-            pg[i] = PagedLoader128<TILE, W, BSM, STREAM>::group_page(p, bt_row, j0 + w * RW + 4 * i,
-                                                                kv_limit);
+            pg[i] = uniform_group_page<BSM>(p, bt_row, j0 + w * RW + 4 * i, kv_limit);
 #pragma unroll
         for (int i = 0; i < VI; ++i)
-            pg[KI + i] = PagedLoader128<TILE, W, BSM, STREAM>::group_page(p, bt_row,
-                                                                     j0 + w * RW + 8 * i, kv_limit);
+            pg[KI + i] = uniform_group_page<BSM>(p, bt_row, j0 + w * RW + 8 * i, kv_limit);
     }
 
     static __device__ __forceinline__ long long group_base(const FaParams &p, long long head_off,
