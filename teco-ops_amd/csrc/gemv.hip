@@ -587,7 +587,13 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
         // and 14.0 -> 13.8 us; waiting for x outright: 14.0 us; fp16 W, twice
         // the bytes per x byte, gains nothing).  With 2 W steps in flight per
         // lane, pauses of 0, 8, 16 and 32 (x 64 cycles) took 13.5-14.0, 13.4,
-        // 12.9-13.1 and 13.3 us on one box.
+        // 12.9-13.1 and 13.3 us on one box.  The best pause is about one
+        // vector L1 -> L2 read round trip of this stream (865 cycles with one
+        // load in flight per lane, 1267 with two; rocprofv3
+        // TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ), i.e. long enough for
+        // x's requests to leave the L1 and L2 queues before the W requests
+        // fill them, and shorter than waiting for x's data (the HBM round
+        // trip, ~2000 cycles once the stream saturates).
         if constexpr (I8) {
             if (ph == 0 && gridDim.x >= 128) __builtin_amdgcn_s_sleep(16);
         }
