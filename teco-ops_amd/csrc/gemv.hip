@@ -796,8 +796,14 @@ constexpr int kRI8 = 2, kCplI8 = 4;
 // at batch 8 on [14336, 4096], same box: int8 with 1, 2, 3, 4, 8 and 16
 // steps in flight took 16.5, 12.6, 13.1, 14.9, 15.9 and 16.3 us (2 row
 // groups per wave: 15.0-15.6 us); fp16 with 2, 4, 6, 8, 10, 12 and 16 took
-// 22.0, 22.5, 21.7, 20.8, 20.9, 21.2 and 20.8 us.
-constexpr int kB8RgF16 = 1, kB8CplF16 = 8, kB8RgI8 = 1, kB8CplI8 = 2;
+// 22.0, 22.5, 21.7, 20.8, 20.9, 21.2 and 20.8 us.  With x staged in one
+// phase fp16 takes 16 (kB8CplF16Whole): three alternating runs on each of two
+// boxes gave 8 / 10 / 12 / 14 / 16 / 20 / 24 in flight 21.07-21.17 / 21.00-
+// 21.04 / 21.5-21.6 / 21.13-21.22 / 20.85-20.97 / 21.9-22.0 / 27.2-27.4 us
+// (no spills at 16; at 24 and more the ring no longer fits the registers);
+// on a third box 16 and 8 tied (21.18-21.25 / 21.22-21.38 us).
+// Phased x keeps 8: its kernels spill 32-64 bytes at 16.
+constexpr int kB8RgF16 = 1, kB8CplF16 = 8, kB8CplF16Whole = 16, kB8RgI8 = 1, kB8CplI8 = 2;
 // Below kB8SmallN rows the grid holds too few waves (4 rows each) to keep HBM
 // busy with 2 int8 steps in flight per lane; 8 then pay.  N = 4096, K = 14336
 // at batch 2 / 4 / 8: 22.1 / 22.6 / 45.0 us with 2, 16.2 / 16.8 / 33.9 with 8;
@@ -936,6 +942,8 @@ bool launch_b8_ncg(const void *W, const void *sc, const void *x, void *y, int B,
     if (nph == 0) return false;
     if (I8 && N < kB8SmallN)
         return launch_b8_cpl<T, I8, NCG, kB8CplI8Small, 1>(W, sc, x, y, B, N, K, nph, s);
+    if (!I8 && nph == 1)
+        return launch_b8_cpl<T, I8, NCG, kB8CplF16Whole, 1>(W, sc, x, y, B, N, K, nph, s);
     return launch_b8_cpl<T, I8, NCG, I8 ? kB8CplI8 : kB8CplF16, 1>(W, sc, x, y, B, N, K, nph, s);
 }
 
