@@ -12,6 +12,8 @@
 //   ./bench_probes wstream    read-only streams with the int8 batch-8 GEMV's
 //                             layout ([14336, 4096] int8, 4 rows per wave),
 //                             CPL 16-byte loads in flight per lane
+//   ./bench_probes convtm     the token-major causal_conv1d's loads and stores
+//                             (window rows included) without its math
 //   ./bench_probes issue      v_exp_f32 / v_fma_f32 issue cost per SIMD with
 //                             1-4 waves per SIMD, and MFMA with exp in one wave
 //   ./bench_probes lds        LDS read bandwidth per CU (ds_read_b128 / b64)
@@ -250,6 +252,80 @@ void wstream() {
     CHECK(hipFree(out));
 }
 
+// ------------------------------------------------------------- convtm
+
+// The token-major causal_conv1d's memory pattern (conv1d_tokens_kernel at the
+// BASELINE shape: x and out [16384 tokens, 4096] fp16) without its math.
+// Work item (chunk, slab) = 8 tokens x 2048 channels, dealt to the XCDs in
+// contiguous ranges; lane: 8 channels (16 bytes) of each row.  WIN: the lane
+// loads the W-1 = 3 rows before its chunk too (plain, as the chunk's last 3
+// rows, which the next chunk re-reads; the other 5 non-temporal) and stores
+// row j as the XOR of rows j .. j+3; else it loads its 8 rows (non-temporal)
+// and stores them.
+template <bool WIN>
+__global__ void __launch_bounds__(256) convtm_kernel(const u32x4 *__restrict__ x,
+                                                     u32x4 *__restrict__ out, long nitems,
+                                                     long per_xcd) {
+    constexpr int CH = 8, WM1 = 3, ROWV = 512;  // 16-byte vectors per row
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (item >= nitems) return;
+    const long t0 = (item / 2) * CH;
+    const int dv = static_cast<int>(item % 2) * 256 + wave * 64 + lane;
+    if (WIN) {
+        u32x4 raw[WM1 + CH];
+#pragma unroll
+        for (int j = 0; j < WM1 + CH; ++j) {
+            long row = t0 - WM1 + j;
+            row = row < 0 ? 0 : row;
+            const u32x4 *p = x + row * ROWV + dv;
+            raw[j] = (j >= WM1 && j < CH) ? __builtin_nontemporal_load(p) : *p;
+        }
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+            __builtin_nontemporal_store(raw[j] ^ raw[j + 1] ^ raw[j + 2] ^ raw[j + 3],
+                                        out + (t0 + j) * ROWV + dv);
+    } else {
+        u32x4 raw[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) raw[j] = __builtin_nontemporal_load(x + (t0 + j) * ROWV + dv);
+#pragma unroll
+        for (int j = 0; j < CH; ++j) __builtin_nontemporal_store(raw[j], out + (t0 + j) * ROWV + dv);
+    }
+}
+
+void convtm() {
+    const long tokens = 16384, bytes = tokens * 4096 * 2;  // x, and out alike
+    const size_t pool_bytes = size_t(3) << 30, span = 2 * bytes;
+    const int rotate = static_cast<int>((size_t(2) << 30) / span) + 1;
+    char *pool;
+    CHECK(hipMalloc(&pool, pool_bytes));
+    CHECK(hipMemset(pool, 1, pool_bytes));
+    const long nitems = tokens / 8 * 2, per_xcd = (nitems + 7) / 8;
+    printf("token-major causal_conv1d pattern, x and out [16384, 4096] fp16 (2 x 134,217,728 B)\n");
+    for (int win = 1; win >= 0; --win) {
+        auto launch = [&](int c) {
+            size_t off = (size_t(c) * span) % (pool_bytes - span);
+            off &= ~size_t(4095);
+            const u32x4 *a = reinterpret_cast<const u32x4 *>(pool + off);
+            u32x4 *b = reinterpret_cast<u32x4 *>(pool + off + bytes);
+            if (win)
+                hipLaunchKernelGGL((convtm_kernel<true>), dim3(8 * per_xcd), dim3(256), 0, 0, a, b,
+                                   nitems, per_xcd);
+            else
+                hipLaunchKernelGGL((convtm_kernel<false>), dim3(8 * per_xcd), dim3(256), 0, 0, a, b,
+                                   nitems, per_xcd);
+        };
+        const double us = time_launches(launch, rotate);
+        printf("  %-58s %7.2f us  %5.3f of 8 TB/s\n",
+               win ? "11 rows loaded (3 re-read from L2), 8 stored per lane" :
+                     "8 rows loaded, 8 stored per lane (same grid, no window)",
+               us, 2.0 * bytes / us / 1e6 / 8.0);
+        fflush(stdout);
+    }
+    CHECK(hipFree(pool));
+}
+
 // --------------------------------------------------------------- issue
 
 // MODE 0: 16 independent exp per iteration, 1: 16 fma, 2: the first half of
@@ -460,10 +536,11 @@ int main(int argc, char **argv) {
     const char *what = argc > 1 ? argv[1] : "";
     if (!strcmp(what, "ceilings")) ceilings();
     else if (!strcmp(what, "wstream")) wstream();
+    else if (!strcmp(what, "convtm")) convtm();
     else if (!strcmp(what, "issue")) issue();
     else if (!strcmp(what, "lds")) lds();
     else {
-        fprintf(stderr, "usage: %s ceilings | wstream | issue | lds\n", argv[0]);
+        fprintf(stderr, "usage: %s ceilings | wstream | convtm | issue | lds\n", argv[0]);
         return 2;
     }
     return 0;
