@@ -383,10 +383,11 @@ def test_prefill_long_query_ranges(dt, H, Hkv):
 @pytest.mark.parametrize("bs,H,Hkv", [(24, 8, 2), (5, 6, 3), (1, 5, 5)])
 def test_prefill_long_query_ranges_generic_loader(bs, H, Hkv):
     """D = 128 query ranges above 1024 rows with block sizes that are not a
-    power of two of at least 8 take the 12-wave kernel with the generic
-    loader (one block-table lookup per row): ragged lengths, a cached prefix,
-    a sequence shorter than one tile, GQA groups of 4, 2 and 1, and a
-    max_seqlen_q hint below the longest range."""
+    power of two of at least 8 take the 12-wave kernel: block 24 with the
+    page-uniform HBM -> LDS copy and a division for the block lookup, blocks
+    5 and 1 with the generic loader (one block-table lookup per row); ragged
+    lengths, a cached prefix, a sequence shorter than one tile, GQA groups of
+    4, 2 and 1, and a max_seqlen_q hint below the longest range."""
     q_lens, kv = [1100, 1537, 40, 1300], [1100, 2000, 900, 1300]
     q, kc, vc, bt = make_inputs(110 + bs + H, H, Hkv, 128, bs, q_lens, kv, dtype=orc.HALF)
     ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=orc.HALF)
@@ -578,6 +579,40 @@ def test_decode_from_two_threads():
     for i, (q, kc, vc, bt, kv) in enumerate(jobs):
         ref = orc.flash_attention(q, kc, vc, bt, [1] * 32, kv, dtype=orc.BF16)
         assert_close(outs[i], ref, what=f"thread {i}")
+
+
+@pytest.mark.parametrize("dt", [orc.HALF, orc.BF16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("bs", [16, 24])
+@pytest.mark.parametrize("kind", ["prefill_12wave", "prefill_32row", "decode"])
+def test_nan_in_cache_slots_past_kv_len(kind, bs, dt):
+    """Cache slots past each sequence's kv_len (the rest of its last block) and
+    blocks no sequence uses hold NaN, as stale cache memory may: the kernels
+    never let them reach the output.  The tile loaders copy 4- or 8-row groups
+    that straddle kv_len (kv lengths that are not multiples of 4), the K rows
+    past it are masked in the softmax and the V rows past it are replaced by
+    zeros (the prefill's HBM -> LDS copy reads them from a zero constant, the
+    decode zeroes them when it stores the tile), so a NaN there would turn a
+    whole output row into NaN (0 * NaN).  Block sizes 16 (a power of two) and
+    24 (a multiple of 8) take the two block-lookup modes."""
+    q_lens, kv = {"prefill_12wave": ([1100, 1301], [1101, 1303]),
+                  "prefill_32row": ([70, 129, 5], [73, 1030, 6]),
+                  "decode": ([1, 1, 1], [77, 1501, 3])}[kind]
+    q, kc, vc, bt = make_inputs(7 + bs, 8, 2, 128, bs, q_lens, kv,
+                                num_blocks=sum(-(-s // bs) for s in kv) + 3, dtype=dt)
+    nan = np.uint16(0x7E00 if dt == orc.HALF else 0x7FC0)
+    used = set()
+    for b, s in enumerate(kv):
+        nblk = -(-s // bs)
+        used.update(int(p) for p in bt[b, :nblk])
+        last, tail = int(bt[b, nblk - 1]), s - (nblk - 1) * bs
+        kc[last, :, tail:, :] = nan
+        vc[last, :, tail:, :] = nan
+    for p in set(range(kc.shape[0])) - used:
+        kc[p], vc[p] = nan, nan
+    ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=dt)
+    got = run_gpu(q, kc, vc, bt, q_lens, kv, dt)
+    assert np.isfinite(got).all(), f"{kind} bs={bs}: NaN from cache slots past kv_len"
+    assert_close(got, ref, what=f"{kind} bs={bs} NaN past kv_len")
 
 
 @pytest.mark.parametrize("H,Hkv", [(40, 8), (64, 8)])
