@@ -1136,11 +1136,11 @@ __device__ __attribute__((noinline)) void prefill_rest(const KernargParams *pp, 
 // W >= 12 asks for 3 waves per SIMD (168 VGPRs); head sizes above 128 with 4
 // waves one (their 4-wave tiles fill the registers), else 2.
 //
-// The grid has one tile row more than max_seqlen_q asks for; that bound is
-// one the reference never reads (flash_attention.cpp:98-99).  Its workgroups
-// are dispatched last and take every query tile past the other rows, in
-// turn.  With a bound that holds there is none, and they exit at once while
-// the tail of the grid drains: a prefill is one launch whatever the bound.
+// The grid's tile rows are sized from max_seqlen_q, a bound the reference
+// never reads (flash_attention.cpp:98-99).  The workgroup of tile 0, which
+// is dispatched last, then takes every query tile past the grid in turn;
+// with a bound that holds there is none.  A prefill is one launch whatever
+// the bound.
 template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
 __global__ void __launch_bounds__(W * 64, (W >= 12 || TILE == 32) ? 3 : (D > 128 && W < 8 ? 1 : 2))
 fa_prefill_kernel(FaParams p) {
@@ -1151,21 +1151,17 @@ fa_prefill_kernel(FaParams p) {
     const int hg = blockIdx.x % ngroups;
     const int kvh = (blockIdx.x / ngroups) % p.Hkv;
     const int b = blockIdx.x / ngroups / p.Hkv;
-    const int rows = gridDim.y - 1;  // tile rows sized from max_seqlen_q
+    const int rows = gridDim.y;  // tile rows sized from max_seqlen_q
     long long q_off;
     int L;
     seq_info(p, b, q_off, L);
     const int S = kv_len(p, b);
-    if (blockIdx.y == rows) {
-        if (rows * QT < L)
-            prefill_rest<T, D, W, HW, QSUB, BSM, TILE>(
-                (const KernargParams *)(__builtin_amdgcn_kernarg_segment_ptr()), b, kvh,
-                hg, rows);
-        return;
-    }
     const int tile = rows - 1 - blockIdx.y;  // heaviest causal tiles first
-    if (tile * QT >= L) return;
-    prefill_tile<T, D, W, HW, QSUB, BSM, TILE>(p, lds, b, kvh, hg, q_off, L, S, tile * QT);
+    if (tile * QT < L)
+        prefill_tile<T, D, W, HW, QSUB, BSM, TILE>(p, lds, b, kvh, hg, q_off, L, S, tile * QT);
+    if (tile == 0 && rows * QT < L)
+        prefill_rest<T, D, W, HW, QSUB, BSM, TILE>(
+            (const KernargParams *)(__builtin_amdgcn_kernarg_segment_ptr()), b, kvh, hg, rows);
 }
 
 // ----------------------------------------------------------------- decode
@@ -1589,7 +1585,7 @@ size_t workspace_bytes(const Plan &pl, int batch, int Hkv, int D) {
 }
 
 // Prefill over a grid of ceil(q_hint / QT) query tiles per (b, kv head, head
-// group), plus the row that covers any tiles past them.
+// group); the workgroups of tile 0 cover any tiles past them.
 template <typename T, int D, int W, int HW, int QSUB, int BSM, int TILE>
 tecoopsStatus_t launch_prefill(const FaParams &p, const Plan &pl, hipStream_t s) {
     constexpr int QT = 32 * QSUB * (W / HW);
@@ -1599,7 +1595,7 @@ tecoopsStatus_t launch_prefill(const FaParams &p, const Plan &pl, hipStream_t s)
         return TECOOPS_STATUS_INTERNAL_ERROR;
     const int units = p.batch * p.Hkv * (p.G / HW);
     const int tiles = (pl.rq + QT - 1) / QT;
-    hipLaunchKernelGGL(kern, dim3(units, tiles + 1), dim3(W * 64), lds, s, p);
+    hipLaunchKernelGGL(kern, dim3(units, tiles), dim3(W * 64), lds, s, p);
     TECO_CHECK_LAUNCH("flash_attention prefill");
     return TECOOPS_STATUS_SUCCESS;
 }
