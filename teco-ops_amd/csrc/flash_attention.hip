@@ -1131,8 +1131,9 @@ __device__ __attribute__((noinline)) void prefill_rest(const KernargParams *pp, 
 
 // Workgroup (b, kv head, head group, query tile) with W waves: wave w serves
 // query head hg*HW + w % HW of the GQA group and query rows
-// [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of TILE keys are double
-// buffered in LDS (one barrier per tile) and attended 32 * NKB keys at a time.
+// [q0 + (w / HW) * 32*QSUB, +32*QSUB).  K/V tiles of TILE keys rotate through
+// the loader's LDS buffers (three for the HBM -> LDS copy, two for register
+// staging; one barrier per tile) and are attended 32 * NKB keys at a time.
 // W >= 12 asks for 3 waves per SIMD (168 VGPRs); head sizes above 128 with 4
 // waves one (their 4-wave tiles fill the registers), else 2.
 //
