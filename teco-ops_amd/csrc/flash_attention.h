@@ -36,12 +36,12 @@ struct FaParams {
 };
 
 // Launch shape.  rq is the host's bound on q_len (routing and grid height),
-// split_len / max_splits the split-KV plan from its bound on kv_len.  Neither
-// bound changes the output (the kernels also cover longer sequences), only
-// the speed.
+// rk its bound on kv_len (prefill routing), split_len / max_splits the
+// split-KV plan from rk.  Neither bound changes the output (the kernels also
+// cover longer sequences), only the speed.
 struct Plan {
     bool decode;
-    int rq, ncols, split_len, max_splits;
+    int rq, rk, ncols, split_len, max_splits;
 };
 
 // A validated call: kernel parameters, launch shape and element type.

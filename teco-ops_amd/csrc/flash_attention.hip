@@ -1562,6 +1562,7 @@ Plan make_plan(int batch, int H, int Hkv, int q_hint, int k_hint) {
     const int G = H / Hkv;
     pl.decode = q_hint >= 1 && G * q_hint <= 32;
     pl.rq = q_hint;
+    pl.rk = k_hint;
     pl.ncols = G * q_hint;
     // Split the key range so that the grid has at least ~512 workgroups (one
     // per slot of the 256 CUs, two each), with splits as long as that allows:
@@ -1609,6 +1610,40 @@ tecoopsStatus_t prefill_hw(const FaParams &p, const Plan &pl, hipStream_t s) {
     return launch_prefill<T, D, W, 1, QSUB, BSM, TILE>(p, pl, s);
 }
 
+// D = 128 prefill route for a query bound of at most 1024 rows: true takes
+// the 12-wave kernel (96-row tiles, one workgroup per CU), false the 4-wave
+// kernel over 32-row tiles (three per CU).  Over a long cached context the
+// 12-wave kernel is ~10 % faster per row and key (each K/V tile serves
+// three times the rows), but it pads rows to 96 and has a third of the
+// workgroup slots.  So it is taken when the context is long (keys at least
+// 4x the rows, or 2x and 2048 or more), its grid covers most CUs (160
+// workgroups on 256 CUs), and it needs no more dispatch rounds (workgroups
+// over slots, rounded up) than the 32-row kernel.  bf16 H32 Hkv8 causal
+// block 16, µs 32-row / 12-wave (batch x query rows / keys):
+//   taken: 64 x 64 / 4096 409 / 387, 64 x 96 / 4096 590 / 417, 16 x 256 /
+//     4096 354 / 325, 8 x 512 / 4096 323 / 293, 16 x 512 / 2048 291 / 267,
+//     8 x 1024 / 2048 246 / 219, 8 x 1024 / 4096 547 / 471, 2 x 1024 /
+//     16384 (176 workgroups) 585 / 551, 32 x 256 / 1024 168 / 163, 12 x 700
+//     / 4096 605 / 509, 40 x 160 / 4096 594 / 530
+//   more rounds: 24 x 250 / 1000 (3 against 2) 120 / 135, 64 x 128 / 1024
+//     196 / 222, 64 x 16 / 4096 205 / 358
+//   short context: 32 x 256 / 512 88 / 99, 64 x 96 / 192 40 / 42, 64 x 256
+//     / 256 105 / 118, 32 x 512 / 512 129 / 152, 16 x 1024 / 1024 191 / 190
+//   under 160 workgroups: 4 x 256 / 16384 (96) 434 / 510, 16 x 64 / 16384
+//     (128) 443 / 521, 3 x 1024 / 16384 (2 rounds against 1) 830 / 1118
+//   where the rule misses: 48 x 200 / 2000 (5 rounds against 4) 482 / 454,
+//     6 x 256 / 16384 (144 workgroups) 528 / 516, 16 x 512 / 1024 137 / 135
+bool prefill_wide(const FaParams &p, const Plan &pl) {
+    const long long q = pl.rq, k = pl.rk;
+    if (k < 2 * q || (k < 4 * q && k < 2048)) return false;
+    const int hw = p.G % 4 == 0 ? 4 : (p.G % 2 == 0 ? 2 : 1);
+    const long long units = static_cast<long long>(p.batch) * p.Hkv * (p.G / hw);
+    const long long n12 = units * ((q + 95) / 96), n4 = units * ((q + 31) / 32);
+    const long long cus = tecoops::device_cus();
+    if (n12 * 256 < 160 * cus) return false;
+    return (n12 + cus - 1) / cus <= (n4 + 3 * cus - 1) / (3 * cus);
+}
+
 template <typename T, int D>
 tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
     // Block-size mode (block_of): the uniform-page loaders take block sizes
@@ -1637,17 +1672,17 @@ tecoopsStatus_t run(hipStream_t s, const FaParams &p, const Plan &pl) {
         // over 96 query rows and 96-key tiles.  Up to 1024 query rows (short
         // prompts, chunks over a cached context): 4 waves over 32 rows and
         // 32-key tiles, three workgroups per CU, which wastes fewer masked
-        // rows and hides each workgroup's start-up behind the others.  bf16,
-        // H32 Hkv8, µs 12-wave / 4-wave: 64 x 16 rows over 4096 keys 446 /
-        // 278, 64 x 32 408 / 249, 16 x 256 384 / 354, 8 x 512 341 / 327,
-        // prefill 16 x 1024 220 / 206, 4 x 4096 643 / 689, 1 x 16384 2162 /
-        // 2370.
+        // rows and hides each workgroup's start-up behind the others, unless
+        // prefill_wide finds a long cached context and a full grid.  bf16
+        // H32 Hkv8, µs 12-wave / 4-wave: 4 x 4096 643 / 689, 1 x 16384
+        // 2162 / 2370.
+        const bool wide = pl.rq > 1024 || prefill_wide(p, pl);
         if (bsm == 1) {
-            if (pl.rq <= 1024) return prefill_hw<T, D, 4, 1, 1, 32>(p, pl, s);
+            if (!wide) return prefill_hw<T, D, 4, 1, 1, 32>(p, pl, s);
             return prefill_hw<T, D, 12, 1, 1, 96>(p, pl, s);
         }
         if (bsm == 2) {  // block 24, µs mode 0 / 2: B4 S4096 606 / 587, B16 S1024 244 / 208
-            if (pl.rq <= 1024) return prefill_hw<T, D, 4, 1, 2, 32>(p, pl, s);
+            if (!wide) return prefill_hw<T, D, 4, 1, 2, 32>(p, pl, s);
             return prefill_hw<T, D, 12, 1, 2, 96>(p, pl, s);
         }
         // other block sizes (the generic loader): the 12-wave kernel above

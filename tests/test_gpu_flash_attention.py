@@ -396,6 +396,30 @@ def test_prefill_long_query_ranges_generic_loader(bs, H, Hkv):
         assert_close(got, ref, what=f"bs={bs} long query ranges H={H} Hkv={Hkv} max_q={max_q}")
 
 
+@pytest.mark.parametrize("bs,dt", [(16, orc.BF16), (24, orc.HALF)], ids=["bs16-bf16", "bs24-fp16"])
+def test_prefill_chunks_over_cached_context(bs, dt):
+    """D = 128 query chunks of at most 1024 rows over a cached context at
+    least four times as long, with enough workgroups to cover most CUs, take
+    the 12-wave kernel (block 16: power-of-two pages; block 24: the
+    page-uniform copy with a division): 14 sequences, H16 Hkv4, ragged
+    chunks of 7-250 rows over 900-1250 keys.  A bound of 250 rows gives 3
+    tiles of 96 rows and 14 x 4 x 3 = 168 workgroups, a bound of 300 rows 4
+    tiles (224 workgroups, the last tile row empty).  The same inputs with a
+    key bound of 600 (under four times the rows) take the 4-wave kernel over
+    32-row tiles."""
+    r = np.random.default_rng(5)
+    q_lens = r.integers(150, 251, 14).tolist()
+    q_lens[0], q_lens[5] = 250, 7
+    kv = [q + int(r.integers(750, 1001)) for q in q_lens]
+    kv[0] = 1250
+    q, kc, vc, bt = make_inputs(140 + bs, 16, 4, 128, bs, q_lens, kv, dtype=dt)
+    ref = orc.flash_attention(q, kc, vc, bt, q_lens, kv, dtype=dt)
+    for max_q, max_k in ((250, 1250), (300, 1250), (250, 600)):
+        got = run_gpu(q, kc, vc, bt, q_lens, kv, dt, max_q=max_q, max_k=max_k)
+        assert_close(got, ref, what=f"bs={bs} chunks over a cached context max_q={max_q} "
+                                    f"max_k={max_k}")
+
+
 @pytest.mark.parametrize("D", [64, 96, 32, 160, 192])
 @pytest.mark.parametrize("H,Hkv,bs", [(8, 2, 16), (6, 3, 8), (5, 5, 32), (8, 4, 5), (8, 2, 24)])
 def test_prefill_long_query_ranges_other_head_sizes(D, H, Hkv, bs):
