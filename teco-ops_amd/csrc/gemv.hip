@@ -789,6 +789,17 @@ constexpr int kB8Batch2MinK = 10240;
 // took 16.2 us, and 8 or 16 waves per workgroup were slower for both types.
 constexpr int kR16 = 1, kCpl16 = 8;
 constexpr int kRI8 = 2, kCplI8 = 4;
+// int8 at batch 1 with rows of at most kRI8OneMaxK values and at least
+// kRI8OneMinN rows: one row per wave (the whole 4 KiB row in flight, twice
+// the workgroups, half the bytes in flight per wave).  Standalone sweep, 16
+// rotating weight copies, µs two rows / one row per wave: [14336, 4096]
+// 10.57-10.69 / 10.46-10.57 on four boxes, [28672, 4096] 18.5-19.2 /
+// 18.1-19.0, [11008, 4096] 9.0-9.2 / 8.7; at fewer rows or longer rows two
+// stay: [8192, 4096] 7.1-7.2 / 7.3, [4096, 4096] 4.7-5.0 / 5.2-5.5,
+// [14336, 14336] 33.5-36.0 / 35.0-37.2, [8192, 28672] 40-43 / 47-50 (some
+// shapes outside the rule gain: [8192, 8192] 13.3-13.7 / 12.4-12.8,
+// [4096, 14336] 12.4-13.0 / 12.1-12.5).
+constexpr int kRI8OneMaxK = 4096, kRI8OneMinN = 10240;
 
 // 4x4x4 path: groups of 4 rows per wave and load steps in flight per lane,
 // for fp16 / int8 W.  x is staged in LDS once per workgroup, so workgroups
@@ -966,11 +977,11 @@ bool launch16(const void *W, const void *x, void *y, int N, int K, hipStream_t s
     return true;
 }
 
-template <int B>
-bool launch_i8(const void *W, const void *sc, const void *x, void *y, int N, int K,
-               hipStream_t s) {
-    const unsigned grid = tecoops::ceil_div(N, kWaves * kRI8);
-    auto *kern = &gemv_i8_kernel<B, kRI8, kCplI8, kWaves>;
+template <int B, int R>
+bool launch_i8_r(const void *W, const void *sc, const void *x, void *y, int N, int K,
+                 hipStream_t s) {
+    const unsigned grid = tecoops::ceil_div(N, kWaves * R);
+    auto *kern = &gemv_i8_kernel<B, R, kCplI8, kWaves>;
     if (!tecoops::reserve_lds(reinterpret_cast<const void *>(kern), B * static_cast<size_t>(K) * 2))
         return false;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads),
@@ -978,6 +989,13 @@ bool launch_i8(const void *W, const void *sc, const void *x, void *y, int N, int
                        static_cast<const uint16_t *>(sc), static_cast<const uint4 *>(x),
                        static_cast<uint16_t *>(y), N, K);
     return true;
+}
+
+template <int B>
+bool launch_i8(const void *W, const void *sc, const void *x, void *y, int N, int K,
+               hipStream_t s) {
+    if (B == 1 && K <= kRI8OneMaxK && N >= kRI8OneMinN) return launch_i8_r<B, 1>(W, sc, x, y, N, K, s);
+    return launch_i8_r<B, kRI8>(W, sc, x, y, N, K, s);
 }
 
 template <typename T>

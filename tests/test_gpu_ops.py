@@ -631,6 +631,23 @@ def test_gemv_int8(B):
     assert_close(got, ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2, what=f"gemv_int8 B={B}")
 
 
+@pytest.mark.parametrize("N,K", [(10243, 2000), (10240, 4096), (10239, 4096), (10240, 4112)])
+def test_gemv_int8_batch1_row_split(N, K):
+    """Batch-1 int8 rows of at most 4096 values over at least 10240 rows take
+    one row per wave (workgroups of 4 rows, the last one ragged at N = 10243);
+    one row fewer, or 16 values more per row, takes two rows per wave."""
+    r = rng(450 + N % 7 + K // 16)
+    W = r.integers(-127, 128, (N, K), dtype=np.int8)
+    s = bits(r.uniform(0.001, 0.01, N))
+    x = bits(r.standard_normal((1, K)))
+    ref = orc.gemv_int8(W, s, x)
+    y = torch.empty((1, N), dtype=torch.float16, device="cuda")
+    tecoops.gemv_int8(dev(W), dev(s), dev(x), y)
+    torch.cuda.synchronize()
+    assert_close(as_f32(y), ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-2,
+                 what=f"gemv_int8 1x{N}x{K}")
+
+
 @pytest.mark.parametrize("B,K", [(1, 14336), (2, 14336), (4, 14336), (5, 14336), (8, 14336),
                                  (4, 20480), (3, 24576), (1, 40960)])
 @pytest.mark.parametrize("i8", [False, True], ids=["fp16", "int8"])
