@@ -500,6 +500,30 @@ template <> struct Mma4<bf16> {
     }
 };
 
+// 16 zero bytes: the source of staged x rows past the batch.
+__device__ __attribute__((aligned(16))) const uint32_t kXZero16[4] = {0u, 0u, 0u, 0u};
+
+// Global -> LDS with no register staging: 16 bytes per lane into
+// dst + 16 * lane (dst wave-uniform, in M0).  Inline assembly so that the
+// compiler does not count the copy among its own loads: through the builtin
+// it would wait for every load in flight (the W ring included) before the
+// first LDS read.  The copies are ordered by wait_vm() and the workgroup
+// barrier after it.  No other code of these kernels uses M0.
+__device__ __forceinline__ void dma16(const void *src, void *dst) {
+    const uint32_t lds = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)(dst)));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+                 : "memory");
+}
+
+// s_waitcnt vmcnt(N): all but the N youngest vector-memory operations of the
+// wave are done (expcnt and lgkmcnt not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(((N >> 4) << 14) | 0x0F70 | (N & 15));
+}
+
 // x chunks (16 bytes) a workgroup of the 4x4x4 path loads into registers
 // ahead of its first W loads (64 KiB, the whole x of batch 8 at K = 4096); a
 // larger staged x copies the chunks past these straight to LDS.
@@ -556,6 +580,11 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
             for (int v = 0; v < 4; ++v) sc[g][v] = scales[min(n0 + 4 * g + v, N - 1)];
     }
     constexpr int XPT = (kMaxXChunks + NW * 64 - 1) / (NW * 64);  // x chunks per thread
+    // int8 W with x staged in one phase: x goes straight into LDS (no
+    // registers, no LDS stores).  [14336, 4096] batch 8, three alternating
+    // runs, us register-staged / copied: int8 12.57-12.91 / 12.10-12.43;
+    // fp16 20.92-21.02 / 21.77-21.86, so fp16 keeps the registers.
+    constexpr bool XDMA = I8 && !PHASED;
     const int nxc = NCG * 4 * kxp;
     // This lane's x chunks in LDS: chunk 16i + blk (fp16 W) or 32i + 2blk and
     // the next (int8 W) of row 4cg + r.  The swizzle xor (4r < 16) stays below
@@ -572,12 +601,27 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
     for (int ph = 0; ph < nph; ++ph) {
         const int xc0 = ph * kxp;       // the phase's first chunk of an x row
         const int st0 = ph * nl * KS;   // ... and first load step of a W row
-        uint4 xr[XPT];
+        uint4 xr[XDMA ? 1 : XPT];
+        if constexpr (!XDMA) {
 #pragma unroll
-        for (int j = 0; j < XPT; ++j) {
-            const int idx = min(static_cast<int>(threadIdx.x) + j * NW * 64, nxc - 1);
-            const int row = min(idx / kxp, B - 1);
-            xr[j] = x[static_cast<long long>(row) * kx + xc0 + idx % kxp];
+            for (int j = 0; j < XPT; ++j) {
+                const int idx = min(static_cast<int>(threadIdx.x) + j * NW * 64, nxc - 1);
+                const int row = min(idx / kxp, B - 1);
+                xr[j] = x[static_cast<long long>(row) * kx + xc0 + idx % kxp];
+            }
+        } else {
+            // the whole x straight into LDS: copy m fills LDS chunks [64m, 64m + 64), so lane
+            // l loads the x chunk stored at 64m + l (the swizzle flips bits 2-3 of the chunk
+            // index only, within the copy's 64); rows past the batch copy zeros
+            for (int m = wave; m < nxc / 64; m += NW) {
+                const int slot = 64 * m + lane;
+                const int row = slot / kxp, cs = slot - row * kxp;
+                const void *src = row < B ? static_cast<const void *>(
+                                                x + static_cast<long long>(row) * kx +
+                                                (cs ^ (4 * (row & 3))))
+                                          : static_cast<const void *>(kXZero16);
+                dma16(src, xs_raw + 64 * m);
+            }
         }
         // int8 W on a full-GPU grid: every CU's x loads miss L2 together and,
         // at HBM, queue behind the first W loads of all waves, which start at
@@ -655,6 +699,17 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
             // x larger than the register-staged part (more than 4096 chunks)
             // copies the rest directly
             [&] {
+                if constexpr (XDMA) {
+                    // this wave's copies are older than the W loads issued
+                    // since (ring_steps: CPL steps of RG loads, or one step
+                    // when the row has fewer than CPL, none when it has
+                    // none); the barrier then covers every wave's
+                    if (nl >= CPL) wait_vm<CPL * RG>();
+                    else if (nl > 0) wait_vm<RG>();
+                    else wait_vm<0>();
+                    __syncthreads();
+                    return;
+                }
                 if (ph > 0) __syncthreads();
 #pragma unroll
                 for (int j = 0; j < XPT; ++j) {
