@@ -60,6 +60,71 @@ EXTRA_FLAGS = {
 }
 
 
+# Sources whose kernels copy global memory straight into LDS
+# (global_load_lds_dwordx4, inline assembly) and then wait for the copies
+# with a fixed vmcnt that leaves the compiler's own younger loads in flight.
+# The count is right only if those loads stay between the copies and the
+# wait, which the compiler does not promise for loads of read-only memory,
+# so the device assembly of these sources is checked on every build.
+COPY_WAIT_CHECKED = ["gemv.hip"]
+
+
+def check_copy_waits(asm_text, src=""):
+    """Checks, in each kernel of `asm_text` that copies into LDS, the first
+    vmcnt wait after each run of copies: its count N must not exceed the
+    vector-memory operations issued between the last copy and the wait (so
+    that the copies are among the completed ones, vector-memory loads
+    completing in issue order), no barrier may come between the copies and
+    that wait, and M0 may be written only right before a copy.  Returns the
+    number of waits checked; raises RuntimeError on a violation."""
+    import re
+    checked = 0
+    kernels = list(re.finditer(r"^(_Z\S*):", asm_text, re.M))
+    for m in kernels:
+        end = asm_text.find(".Lfunc_end", m.end())
+        lines = [l.split(";")[0].strip() for l in asm_text[m.end():end].split("\n")]
+        lines = [l for l in lines if l and not l.startswith(".")]
+        if not any(l.startswith("global_load_lds") for l in lines):
+            continue
+        pending, since = False, 0
+        for i, l in enumerate(lines):
+            if re.search(r"\bm0\b", l) and not (l.startswith("s_mov_b32 m0,") and i + 1 < len(lines)
+                                                and lines[i + 1].startswith("global_load_lds")):
+                raise RuntimeError(f"{src}: {m.group(1)}: M0 used outside a copy: {l}")
+            if l.startswith("global_load_lds"):
+                pending, since = True, 0
+                continue
+            if not pending:
+                continue
+            if re.match(r"(global|buffer|flat)_(load|store|atomic)", l):
+                since += 1
+            w = re.match(r"s_waitcnt\b.*\bvmcnt\((\d+)\)", l)
+            if w:
+                if int(w.group(1)) > since:
+                    raise RuntimeError(f"{src}: {m.group(1)}: {l} after copies with only {since} "
+                                       "younger vector-memory operations: the copies may be in flight")
+                pending = False
+                checked += 1
+            elif l.startswith("s_barrier"):
+                raise RuntimeError(f"{src}: {m.group(1)}: barrier before the copies are waited for")
+    return checked
+
+
+def _check_copies(src):
+    out = os.path.join(BUILD, os.path.splitext(src)[0] + ".s")
+    cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(src, []), "--cuda-device-only", "-S",
+           os.path.join(CSRC, src), "-o", out]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"assembly failed: {src}\n{' '.join(cmd)}\n{r.stderr[-4000:]}")
+    with open(out) as f:
+        n = check_copy_waits(f.read(), src)
+    os.remove(out)
+    if n == 0:
+        raise RuntimeError(f"{src}: no copy waits found to check")
+    return out, ""
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
     cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
@@ -129,7 +194,10 @@ def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     jobs = min(len(SOURCES), os.cpu_count() or 4, 16)
     with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
+        checks = [ex.submit(_check_copies, src) for src in COPY_WAIT_CHECKED]
         results = list(ex.map(_compile, SOURCES))
+        for c in checks:
+            c.result()
     for _, err in results:
         if err.strip() and verbose:
             print(err, file=sys.stderr)

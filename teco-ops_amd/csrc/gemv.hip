@@ -508,7 +508,8 @@ __device__ __attribute__((aligned(16))) const uint32_t kXZero16[4] = {0u, 0u, 0u
 // compiler does not count the copy among its own loads: through the builtin
 // it would wait for every load in flight (the W ring included) before the
 // first LDS read.  The copies are ordered by wait_vm() and the workgroup
-// barrier after it.  No other code of these kernels uses M0.
+// barrier after it.  No other code of these kernels uses M0 (build.py checks
+// both in the assembly).
 __device__ __forceinline__ void dma16(const void *src, void *dst) {
     const uint32_t lds = static_cast<uint32_t>(
         reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)(dst)));
@@ -700,12 +701,17 @@ gemv_b8_kernel(const uint4 *__restrict__ W, const uint16_t *__restrict__ scales,
             // copies the rest directly
             [&] {
                 if constexpr (XDMA) {
-                    // this wave's copies are older than the W loads issued
-                    // since (ring_steps: CPL steps of RG loads, or one step
-                    // when the row has fewer than CPL, none when it has
-                    // none); the barrier then covers every wave's
+                    // This wave's copies are older than the CPL steps of RG
+                    // W loads ring_steps issues before start(), so waiting
+                    // until at most those are outstanding leaves them in
+                    // flight.  The compiler could legally sink a load of
+                    // read-only memory below this wait, which would make the
+                    // count too large: build.py checks the assembly of
+                    // every such wait and fails the build if it ever does.
+                    // A row with fewer steps (ring_steps' short path, K <
+                    // 512) waits for everything.  The barrier then covers
+                    // every wave's copies.
                     if (nl >= CPL) wait_vm<CPL * RG>();
-                    else if (nl > 0) wait_vm<RG>();
                     else wait_vm<0>();
                     __syncthreads();
                     return;
