@@ -2,7 +2,8 @@
 check_copy_waits), on hand-written assembly: it must accept a wait that
 leaves only younger loads in flight and reject a wait whose count could
 include the copies, a barrier before the wait, and M0 written for anything
-but a copy."""
+but a copy; in its M0-only mode (flash_attention.hip) it counts copies and
+checks M0 alone."""
 import os
 import sys
 
@@ -53,3 +54,10 @@ def test_m0_outside_a_copy_is_rejected():
 
 def test_kernels_without_copies_are_skipped():
     assert build.check_copy_waits(HEAD + "\ts_waitcnt vmcnt(5)\n\ts_barrier\n" + TAIL) == 0
+
+
+def test_m0_only_mode_counts_copies_and_ignores_waits():
+    body = COPY + COPY + "\ts_waitcnt vmcnt(9)\n\ts_barrier\n"
+    assert build.check_copy_waits(HEAD + body + TAIL, "fa.hip", waits=False) == 2
+    with pytest.raises(RuntimeError, match="M0 used outside"):
+        build.check_copy_waits(HEAD + "\ts_mov_b32 m0, 0\n" + body + TAIL, "fa.hip", waits=False)
