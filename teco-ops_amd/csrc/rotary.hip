@@ -6,7 +6,7 @@
 // theta_i = pos * base^(-2i/rot_dim); NeoX pairs (i, i + rot_dim/2), GPT-J
 // pairs (2i, 2i+1):  o1 = x1 cos - x2 sin,  o2 = x2 cos + x1 sin  (fp32 math).
 //
-// gfx950 design: one workgroup per 4 tokens.  The rot_dim/2 (cos, sin) pairs
+// gfx950 design: one workgroup per token.  The rot_dim/2 (cos, sin) pairs
 // of each token are computed once (accurate sincosf, or read from the cache)
 // into LDS and shared by all H + Hkv heads; each lane then rotates 8 NeoX
 // pairs per task with two 16-byte loads and stores (4 pairs with 8-byte words
@@ -25,9 +25,18 @@ using namespace tecoops::dev;
 constexpr int kThreads = 256;
 constexpr int kMaxHalf = 256;  // rot_dim <= 512
 
-constexpr int kTokensPerBlock = 4;
-constexpr int kRotBatch = 6;  // rotation tasks per thread with loads in flight together
-constexpr int kFusedBatch = 8;  // tasks per thread in flight together, fused kernel
+// One token per workgroup, each thread's (at most two) tasks loaded together
+// before any store.  More tokens per workgroup put more of q and k in flight
+// at once, which the memory system serves slower.  q [8192, 32, 128], k
+// [8192, 8, 128], NeoX, µs rotary / fused rotary + cache (tokens per
+// workgroup, tasks in flight per thread, 256 threads unless noted): 1, 2:
+// 28.5 / 36.3-36.5; 2, 3: 29.4 / 36.6-36.8; 4, 6 (8 fused): 29.4 / 37.0-37.2;
+// 8, 5: 31.8 / 41.7; 16, 10: 34.2 / 43.0; 1 token with 128 / 192 / 320 / 384
+// threads: 29.6-29.7 / 28.9 / 29.1-29.3 / 29.6 (fused 37.5-37.7 / 36.4-36.5
+// / 37.5-37.6 / 42.3).
+constexpr int kTokensPerBlock = 1;
+constexpr int kRotBatch = 2;  // rotation tasks per thread with loads in flight together
+constexpr int kFusedBatch = 2;  // tasks per thread in flight together, fused kernel
 
 // o1 = x1 cos - x2 sin, o2 = x2 cos + x1 sin with the roundings spelled out
 // (one product, then one fused multiply-add), so every kernel that rotates
