@@ -8,8 +8,9 @@
 // gfx950 design, by batch size (rows of x):
 //   * 3-8 (fp16 / bf16) or 2-8 (int8) with K a multiple of 128 / 256: the
 //     4x4x4 matrix-core path ("4x4x4 MFMA path" below).  Each wave streams 4
-//     whole rows of W in 256-byte row segments, x sits in LDS, and the waves
-//     start their sweeps of K at staggered offsets.
+//     whole rows of W in 256-byte row segments, x sits in LDS (int8 W: copied
+//     there straight from memory, no registers), and the waves start their
+//     sweeps of K at staggered offsets.
 //   * larger batches and other K (multiples of 32 / 64): the 16x16x32
 //     matrix-core path ("MFMA path" below), in slices of 16 columns.
 //   * 1-2 and all other shapes: the VALU path, which streams W fastest when
@@ -20,8 +21,8 @@
 //     loads, lane-interleaved
 //     along K so that every load instruction reads a contiguous 1 KiB run of
 //     a row; a lane issues the loads of CPL chunks of each row before using
-//     any (a whole fp16 row, or two int8 rows, in flight per wave at K =
-//     4096), and keeps R x B fp32 partial sums; the products use
+//     any (a whole fp16 row, or one or two int8 rows, in flight per wave at
+//     K = 4096), and keeps R x B fp32 partial sums; the products use
 //     v_dot2_f32_{f16,bf16} (two MACs per instruction, fp32 accumulation).  A
 //     wave reduction through DPP and permlane swaps (wave_sum, no LDS)
 //     finishes each (row, batch) sum.
@@ -1055,7 +1056,8 @@ bool launch_i8_r(const void *W, const void *sc, const void *x, void *y, int N, i
 template <int B>
 bool launch_i8(const void *W, const void *sc, const void *x, void *y, int N, int K,
                hipStream_t s) {
-    if (B == 1 && K <= kRI8OneMaxK && N >= kRI8OneMinN) return launch_i8_r<B, 1>(W, sc, x, y, N, K, s);
+    if constexpr (B == 1)
+        if (K <= kRI8OneMaxK && N >= kRI8OneMinN) return launch_i8_r<B, 1>(W, sc, x, y, N, K, s);
     return launch_i8_r<B, kRI8>(W, sc, x, y, N, K, s);
 }
 
