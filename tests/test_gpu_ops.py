@@ -148,10 +148,10 @@ def test_rotary_variants(is_neox, use_cache):
 
 def test_rotary_wide_heads_tails_and_skips():
     """NeoX 16-byte path: 72 heads x 16 tasks per token (rot_dim 256) make
-    several task rounds per thread; 303 tokens leave a partial last
-    workgroup; with the cos/sin cache, positions past it are left
-    unrotated; without a key only q rotates; rot_dim < head_size leaves the
-    tail untouched."""
+    several task rounds per thread (1152 tasks over the 256 threads of a
+    token's workgroup, 2 in flight at a time); an odd token count (303);
+    with the cos/sin cache, positions past it are left unrotated; without a
+    key only q rotates; rot_dim < head_size leaves the tail untouched."""
     r = rng(31)
     T, H, Hkv, D = 303, 64, 8, 256
     q = bits(r.standard_normal((T, H, D)))
