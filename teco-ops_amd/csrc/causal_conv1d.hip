@@ -515,6 +515,9 @@ __global__ void __launch_bounds__(256) conv1d_short_kernel(ConvArgs a) {
 
 constexpr int kTokChunk = 8;    // tokens per lane (4 measured alike, 16 slower)
 constexpr int kTokSlab = 512;   // channels per wave (64 lanes x 8)
+// Waves per workgroup, each its own 512-channel slab.  [16384, 4096] µs, 1 /
+// 2 / 4 waves: 49.1-49.3 / 49.2-49.3 / 49.6-49.8 (three alternating runs).
+constexpr int kTokWaves = 1;
 
 // A sequence of the global token axis: index b, tokens [s, e); b < 0 when the
 // token lies in no sequence.
@@ -601,8 +604,9 @@ __device__ __forceinline__ void token_row(const ConvArgs &a, const SeqSpan &sp, 
 
 // Channel-contiguous layout ([tokens, dim] rows, dim % 8 == 0, 16-byte
 // aligned rows): work item (chunk, slab) covers tokens [8 chunk, +8) of the
-// global token axis and channels [2048 slab, +2048), wave w and lane l
-// channels [2048 slab + 512 w + 8 l, +8) as one 16-byte vector per token.
+// global token axis and channels [512 kTokWaves slab, +512 kTokWaves), wave
+// w and lane l channels [512 (kTokWaves slab + w) + 8 l, +8) as one 16-byte
+// vector per token.
 // Work items are dealt to the 8 XCDs in contiguous ranges (workgroup n runs
 // on XCD n % 8), so the W-1 rows before a chunk, which the previous chunk
 // loaded, are L2 hits.
@@ -624,7 +628,7 @@ __device__ __forceinline__ void token_row(const ConvArgs &a, const SeqSpan &sp, 
 // the sequence's old conv state, and it writes the new state after its
 // tokens, so no lane reads a state another lane writes.
 template <int W, bool SILU>
-__global__ void __launch_bounds__(256) conv1d_tokens_kernel(ConvArgs a, long long nitems,
+__global__ void __launch_bounds__(kTokWaves * 64) conv1d_tokens_kernel(ConvArgs a, long long nitems,
                                                             long long per_xcd, int nslabs) {
     constexpr int CH = kTokChunk;
     const int lane = threadIdx.x & 63;
@@ -632,7 +636,7 @@ __global__ void __launch_bounds__(256) conv1d_tokens_kernel(ConvArgs a, long lon
     const long long item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (item >= nitems) return;
     const long long t0 = (item / nslabs) * CH;
-    const int d0 = static_cast<int>(item % nslabs) * (4 * kTokSlab) + wave * kTokSlab + lane * 8;
+    const int d0 = static_cast<int>(item % nslabs) * (kTokWaves * kTokSlab) + wave * kTokSlab + lane * 8;
     if (d0 >= a.dim) return;
     const SeqSpan sp = seq_of(a, t0);
     if (sp.b < 0 && t0 >= (a.qsl ? a.qsl[a.batch] : static_cast<long long>(a.batch) * a.seq_len))
@@ -786,11 +790,11 @@ void launch(const ConvArgs &a0, bool seq_contig, long long max_len, hipStream_t 
         // query_start_loc, batch * seq_len without
         const long long tokens = a.qsl ? max_len : static_cast<long long>(a.batch) * a.seq_len;
         const long long chunks = (tokens + kTokChunk - 1) / kTokChunk;
-        const int nslabs = static_cast<int>(tecoops::ceil_div(a.dim, 4 * kTokSlab));
+        const int nslabs = static_cast<int>(tecoops::ceil_div(a.dim, kTokWaves * kTokSlab));
         const long long nitems = chunks * nslabs;
         const long long per_xcd = (nitems + 7) / 8;
         hipLaunchKernelGGL((conv1d_tokens_kernel<W, SILU>), dim3(static_cast<unsigned>(8 * per_xcd)),
-                           dim3(256), 0, s, a, nitems, per_xcd, nslabs);
+                           dim3(kTokWaves * 64), 0, s, a, nitems, per_xcd, nslabs);
         return;
     }
     // mean tokens per sequence: the whole axis over the batch with
