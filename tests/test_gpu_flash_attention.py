@@ -234,19 +234,21 @@ def test_softmax_scale_honoured():
     assert_close(got, ref, what="scale 0.3")
 
 
-def test_baseline_decode_config():
-    """BASELINE decode: bf16, B=64, 32 heads / 8 kv heads, D=128, 1 query token
-    per sequence, paged cache of block 16 with shuffled block ids, seeded
-    context lengths U{512..8192}, q / K / V ~ N(0, 1) as BASELINE.json states.
-    The whole batch is compared with the oracle."""
+@pytest.mark.parametrize("dt", [orc.BF16, orc.HALF], ids=["bf16", "fp16"])
+def test_baseline_decode_config(dt):
+    """BASELINE decode: bf16 (and the same in fp16), B=64, 32 heads / 8 kv
+    heads, D=128, 1 query token per sequence, paged cache of block 16 with
+    shuffled block ids, seeded context lengths U{512..8192}, q / K / V ~ N(0,
+    1) as BASELINE.json states.  The whole batch is compared with the
+    oracle."""
     r = np.random.default_rng(2025)
     kv = r.integers(512, 8193, 64).tolist()
-    q, kc, vc, bt = make_inputs(11, 32, 8, 128, 16, [1] * 64, kv, dtype=orc.BF16,
-                                dist="normal")
-    got = run_gpu(q, kc, vc, bt, [1] * 64, kv, orc.BF16)
-    ref = orc.flash_attention(q, kc, vc, bt, [1] * 64, kv, dtype=orc.BF16)
+    q, kc, vc, bt = make_inputs(11, 32, 8, 128, 16, [1] * 64, kv, dtype=dt, dist="normal")
+    got = run_gpu(q, kc, vc, bt, [1] * 64, kv, dt)
+    ref = orc.flash_attention(q, kc, vc, bt, [1] * 64, kv, dtype=dt)
     assert_close(got, ref, what="decode B=64")
-    assert report("BASELINE decode B=64 N(0,1)", got, ref) <= 1e-2
+    name = "bf16" if dt == orc.BF16 else "fp16"
+    assert report(f"BASELINE decode B=64 N(0,1) {name}", got, ref) <= 1e-2
 
 
 def test_prefill_medium_bf16():
@@ -254,18 +256,19 @@ def test_prefill_medium_bf16():
     check(case, orc.BF16, seed=12)
 
 
-def test_baseline_prefill_config_full():
-    """BASELINE prefill: bf16 q [4, 32, 4096, 128], GQA k/v [4, 8, 4096, 128],
-    causal, q / K / V ~ N(0, 1), pages in shuffled order.  The whole output
-    [16384, 32, 128] is compared with the oracle (all 128 (batch, head)
-    pairs)."""
+@pytest.mark.parametrize("dt", [orc.BF16, orc.HALF], ids=["bf16", "fp16"])
+def test_baseline_prefill_config_full(dt):
+    """BASELINE prefill: bf16 (and the same in fp16) q [4, 32, 4096, 128],
+    GQA k/v [4, 8, 4096, 128], causal, q / K / V ~ N(0, 1), pages in shuffled
+    order.  The whole output [16384, 32, 128] is compared with the oracle
+    (all 128 (batch, head) pairs)."""
     B, H, Hkv, D, S = 4, 32, 8, 128, 4096
-    q, kc, vc, bt = make_inputs(13, H, Hkv, D, 16, [S] * B, [S] * B, dtype=orc.BF16,
-                                dist="normal")
-    got = run_gpu(q, kc, vc, bt, [S] * B, [S] * B, orc.BF16)
-    ref = orc.flash_attention(q, kc, vc, bt, [S] * B, [S] * B, dtype=orc.BF16)
+    q, kc, vc, bt = make_inputs(13, H, Hkv, D, 16, [S] * B, [S] * B, dtype=dt, dist="normal")
+    got = run_gpu(q, kc, vc, bt, [S] * B, [S] * B, dt)
+    ref = orc.flash_attention(q, kc, vc, bt, [S] * B, [S] * B, dtype=dt)
     assert_close(got, ref, what="prefill B=4 S=4096")
-    assert report("BASELINE prefill B4 H32 S4096 N(0,1)", got, ref) <= 1e-2
+    name = "bf16" if dt == orc.BF16 else "fp16"
+    assert report(f"BASELINE prefill B4 H32 S4096 N(0,1) {name}", got, ref) <= 1e-2
 
 
 # ------------------------------------------------------------------------
